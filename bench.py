@@ -1,0 +1,218 @@
+"""Benchmark of the two hot operators on one MI355X.
+
+Headline (``value``): packed varlen FlashAttention forward+backward TFLOP/s on
+configs[1] (H=16, D=128, bf16, 64 sequences with log-uniform lengths in
+[1, 4096], q = k lengths), FLOPs = 4 H D sum(L^2) forward + 10 H D sum(L^2)
+backward.  The same JSON line carries the secondary configurations (split-K
+forward, absorb forward GB/s), the roofline of the dominant kernel measured
+with HIP events on the launch stream, and the CPU baseline (the numpy oracle
+on a bounded sample of the same workload, timed on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_region(fn, iters, stream=None):
+    """Average ms of fn() over iters, with HIP events recorded on the launch stream."""
+    import torch
+    st = stream or torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(iters):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_varlen_c2(steps, warmup):
+    import torch
+    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
+    case = W.config2(seed=0)
+    dev = torch.device("cuda:0")
+    q, k, v, do = W.varlen_tensors(case, dev, with_grad_out=True)
+    cu = W.cu_from_lens(case.q_lens, dev)
+    q.requires_grad_(True), k.requires_grad_(True), v.requires_grad_(True)
+
+    def step():
+        o = packed_varlen_attn(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu)
+        o.backward(do)
+        q.grad = k.grad = v.grad = None
+
+    def fwd():
+        with torch.no_grad():
+            packed_varlen_attn(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    fwd_ms = time_region(fwd, max(steps, 3))
+    flops = case.flops_fwd + case.flops_bwd
+    return case, ms, fwd_ms, flops
+
+
+def bench_varlen_c3(iters):
+    import torch
+    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
+    case = W.config3(seed=0)
+    dev = torch.device("cuda:0")
+    q, k, v = W.varlen_tensors(case, dev)
+    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
+
+    def fwd():
+        with torch.no_grad():
+            packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+
+    fwd()
+    ms = time_region(fwd, iters)
+    del q, k, v
+    torch.cuda.empty_cache()
+    return case, ms
+
+
+def bench_absorb(case, iters):
+    import torch
+    from varlenabsorbflashattn_amd import target_attn_inner, workloads as W
+    from varlenabsorbflashattn_amd.absorb import _project_u
+    dev = torch.device("cuda:0")
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev)
+    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
+    with torch.no_grad():
+        u = _project_u(q_raw, W_Q, W_K).contiguous()
+    scale = 1.0 / math.sqrt(case.D_H)
+
+    def fwd():
+        with torch.no_grad():
+            target_attn_inner(u, X, W_V, cq, ck, scale)
+
+    fwd()
+    ms = time_region(fwd, iters)
+    del q_raw, X, u
+    torch.cuda.empty_cache()
+    return ms
+
+
+def cpu_baseline(budget_s=15.0):
+    """Oracle (numpy fp32) fwd+bwd on the shortest-first prefix of C2's segments
+    that fits the time budget; reported as TFLOP/s of that sample."""
+    import numpy as np
+    from oracle import varlen as ov
+    from varlenabsorbflashattn_amd import workloads as W
+    case = W.config2(seed=0)
+    rng = np.random.default_rng(0)
+    order = np.argsort(case.q_lens)
+    done_flops, t_used, n = 0.0, 0.0, 0
+    H, D = case.H, case.D
+    for i in order:
+        L = int(case.q_lens[i])
+        q, k, v, do = (rng.standard_normal((L, H, D), dtype=np.float32) for _ in range(4))
+        cu = np.array([0, L])
+        t0 = time.perf_counter()
+        ov.forward(q, k, v, cu, cu, 1.0 / math.sqrt(D))
+        ov.backward(q, k, v, do, cu, cu, 1.0 / math.sqrt(D))
+        dt = time.perf_counter() - t0
+        t_used += dt
+        done_flops += 14.0 * H * D * L * L
+        n += 1
+        if t_used > budget_s:
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": done_flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"numpy fp32 oracle fwd+bwd on the {n} shortest of C2's 64 segments "
+                      f"(sum L^2 share {done_flops / (14.0 * H * D * float(np.dot(case.q_lens, case.q_lens))):.3f}), "
+                      f"{t_used:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the operators have no multi-GPU path "
+              "(sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    case, ms, fwd_ms, flops = bench_varlen_c2(args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    fwd_tflops = case.flops_fwd / (fwd_ms * 1e-3) / 1e12
+    log(f"C2 fwd+bwd {ms:.3f} ms/step -> {tflops:.1f} TFLOP/s; fwd {fwd_ms:.3f} ms -> "
+        f"{fwd_tflops:.1f} TFLOP/s")
+    secondary = {}
+    if not args.skip_secondary:
+        from varlenabsorbflashattn_amd import workloads as W
+        c3, c3_ms = bench_varlen_c3(max(3, args.steps // 2))
+        secondary["c3_varlen_splitk_fwd"] = {
+            "ms": c3_ms, "GB/s": c3.bytes_fwd() / (c3_ms * 1e-3) / 1e9,
+            "hbm_frac": c3.bytes_fwd() / (c3_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "TFLOP/s": c3.flops_fwd / (c3_ms * 1e-3) / 1e12}
+        log("C3", secondary["c3_varlen_splitk_fwd"])
+        for cfg in (W.config4(seed=0), W.config5(seed=0)):
+            a_ms = bench_absorb(cfg, max(3, args.steps // 2))
+            gbs = cfg.bytes_fwd() / (a_ms * 1e-3) / 1e9
+            secondary[cfg.name + "_fwd"] = {
+                "ms": a_ms, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+                "TFLOP/s": cfg.flops_fwd / (a_ms * 1e-3) / 1e12,
+                "sum_lq": int(sum(cfg.q_lens)), "sum_lk": int(sum(cfg.k_lens))}
+            log(cfg.name, secondary[cfg.name + "_fwd"])
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    out = {
+        "metric": "varlen-FA fwd/bwd TFLOP/s + absorb-attn HBM GB/s, % of MI355X peak",
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: varlen FA fwd+bwd, bf16, H=16, D=128, 64 seqs "
+                               "log-uniform[1,4096], q=k lens, non-causal",
+                   "seed": 0, "sum_L": int(sum(case.q_lens)),
+                   "sum_L2": int(sum(x * x for x in case.q_lens))},
+        "roofline": {"bound": "mfma", "kernel": "varlen_fwd_kernel<bf16,128>",
+                     "achieved": fwd_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": fwd_tflops / BF16_PEAK_TFLOPS, "traffic": None},
+        "secondary": secondary,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

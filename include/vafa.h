@@ -1,0 +1,166 @@
+/*
+ * vafa.h -- C ABI of the MI355X (gfx950) implementation of packed varlen
+ * FlashAttention and absorbed ragged target attention.
+ *
+ * Every entry point is plain C: device pointers, int64 sizes, a dtype enum,
+ * a caller-owned workspace and a hipStream_t passed as void*.  Calls are
+ * asynchronous on that stream, never allocate device memory and never sync
+ * the host.  They return VAFA_OK (0) or a negative status; the message for
+ * the last failure on the calling thread is available from
+ * vafa_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   fa/ = triton_fa_varlen_v2/triton_fa_varlen_v2/
+ *   ta/ = triton_target_attn_absorb/triton_target_attn_absorb/
+ */
+#ifndef VAFA_H_
+#define VAFA_H_
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define VAFA_API __attribute__((visibility("default")))
+#else
+#define VAFA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define VAFA_OK 0
+#define VAFA_ERR_VALUE (-1)     /* maps to Python ValueError               */
+#define VAFA_ERR_ASSERT (-2)    /* maps to Python AssertionError           */
+#define VAFA_ERR_RUNTIME (-3)   /* HIP launch/runtime failure              */
+#define VAFA_ERR_WORKSPACE (-4) /* workspace too small or misaligned       */
+#define VAFA_ERR_CAPACITY (-5)  /* host output buffer too small            */
+
+/* ---- dtypes -------------------------------------------------------------- */
+#define VAFA_F32 0
+#define VAFA_F16 1
+#define VAFA_BF16 2
+
+/* ---- misc ---------------------------------------------------------------- */
+VAFA_API const char *vafa_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+VAFA_API const char *vafa_last_error(void);
+
+/* ======================================================================== */
+/* Host metadata (pure C++, no device access; usable without a GPU).        */
+/* ======================================================================== */
+
+/* Replaces fa/interface.py:74-93 (_seqinfo_to_cu_seqlens).
+ * seqinfo[n] -> cu_out[n+1] int32; VAFA_ERR_VALUE for n==0, a negative
+ * length or a total above INT32_MAX. */
+VAFA_API int vafa_seqinfo_to_cu(const int64_t *seqinfo, int64_t n, int32_t *cu_out);
+
+/* Replaces fa/interface.py:96-118 and ta/interface.py:92-106
+ * (_validate_cu_seqlens): n1 >= 2, cu[0]==0, cu[n1-1]==T, non-decreasing.
+ * `name` is used in the error message. */
+VAFA_API int vafa_validate_cu(const int64_t *cu, int64_t n1, int64_t T, const char *name);
+
+/* Replaces ta/interface.py:109-116 (_validate_active_segments_have_keys). */
+VAFA_API int vafa_check_active_have_keys(const int64_t *cu_q, const int64_t *cu_k, int64_t n1);
+
+/* Replaces fa/chunk_indices.py:25-65 and ta/chunk_indices.py:19-54
+ * (_prepare_chunk_indices): rows (seg, block) for block < ceil(L/BT).
+ * out holds cap rows of 2 int32; *n_rows receives the row count (also when
+ * VAFA_ERR_CAPACITY is returned). */
+VAFA_API int vafa_chunk_indices(const int64_t *cu, int64_t n1, int32_t BT, int32_t *out,
+                       int64_t cap, int64_t *n_rows);
+
+/* ======================================================================== */
+/* Work plans.                                                              */
+/*                                                                          */
+/* A plan is a flat int32 array built on the host from host copies of       */
+/* cu_seqlens and copied once to the device.  It replaces the reference's   */
+/* SplitIndices / chunk-index tables (fa/chunk_indices.py:144-287,          */
+/* ta/chunk_indices.py:19-67).  Items hold absolute token offsets, are      */
+/* ordered longest-first and every long-tail (segment, q-tile) is split     */
+/* over the key axis; the combine tables merge the split partials.          */
+/* ======================================================================== */
+
+#define VAFA_ITEM_INTS 8 /* every work item is 8 int32 (32 bytes) */
+#define VAFA_PLAN_MAGIC 0x56414641 /* "VAFA" */
+
+typedef struct vafa_plan_info {
+  int64_t magic;          /* VAFA_PLAN_MAGIC */
+  int64_t kind;           /* 1 = varlen, 2 = absorb */
+  int64_t n_seg;
+  int64_t T_q, T_k, H;
+  /* section offsets (in int32 units from the plan start) and item counts */
+  int64_t off_fwd, n_fwd;         /* forward / dq items (query tiles)      */
+  int64_t off_comb, n_comb;       /* combine items                         */
+  int64_t off_kv, n_kv;           /* key-tile items (dK/dV, absorb dX)     */
+  int64_t off_qt, n_qt;           /* unsplit query tiles (absorb dU pass)  */
+  int64_t n_part_rows;            /* partial rows written by split items   */
+  int64_t plan_ints;              /* total plan length in int32            */
+  int64_t q_tile, k_tile;         /* tile sizes the plan was built for     */
+  int64_t max_split;              /* largest number of splits of one tile  */
+} vafa_plan_info;
+
+/* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).
+ * cu_q/cu_k: host int64 [n1].  D selects tile sizes.  Call with plan==NULL
+ * to size (info->plan_ints), then with a buffer of that many int32. */
+VAFA_API int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H,
+                     int64_t D, int32_t *plan, int64_t plan_cap, vafa_plan_info *info);
+
+/* Plan for packed_target_attn (ta/interface.py:191-216, 265-314). */
+VAFA_API int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H,
+                     int64_t D_KV, int64_t D_H, int32_t *plan, int64_t plan_cap,
+                     vafa_plan_info *info);
+
+/* ======================================================================== */
+/* Device entry points.  plan_dev is the plan copied to device memory.      */
+/* workspace: device memory of at least the size the *_workspace query     */
+/* returns, 256-byte aligned.  stream: hipStream_t.                          */
+/* ======================================================================== */
+
+/* Workspace bytes needed by vafa_varlen_fwd / vafa_varlen_bwd. */
+VAFA_API int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D);
+VAFA_API int64_t vafa_varlen_bwd_workspace(const vafa_plan_info *info, int64_t D);
+
+/* Replaces _PackedVarlenAttnFunction.forward (fa/interface.py:153-250):
+ * q [T_q,H,D], k/v [T_k,H,D] contiguous, o [T_q,H,D] (same dtype),
+ * lse [T_q,H] fp32 log2-domain.  D in {16,32,64,128,256}. */
+VAFA_API int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream);
+
+/* Replaces _PackedVarlenAttnFunction.backward (fa/interface.py:252-341):
+ * dO [T_q,H,D] -> dq, dk, dv (same dtype as q). Deterministic (no atomics). */
+VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream);
+
+/* Workspace bytes needed by vafa_absorb_fwd / vafa_absorb_bwd. */
+VAFA_API int64_t vafa_absorb_fwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);
+VAFA_API int64_t vafa_absorb_bwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);
+
+/* Replaces _TargetAttnFunction.forward (ta/interface.py:153-223):
+ * u [T_q,H,D_KV], X [T_k,D_KV], W_V [D_KV,H,D_H] -> O [T_q,H,D_H],
+ * lse [T_q,H] fp32 log2-domain. */
+VAFA_API int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, float *lse,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D_KV,
+                    int64_t D_H, int32_t dtype, float scale, void *workspace,
+                    int64_t workspace_bytes, void *stream);
+
+/* Replaces _TargetAttnFunction.backward (ta/interface.py:225-321):
+ * -> du [T_q,H,D_KV], dX [T_k,D_KV], dW_V [D_KV,H,D_H] (input dtype).
+ * Deterministic: dX and dW_V are reduced in a fixed order (the reference
+ * uses fp32 atomics for dW_V, ta/kernels.py:493). */
+VAFA_API int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O,
+                    const void *dO, const float *lse, void *du, void *dX, void *dW_V,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D_KV,
+                    int64_t D_H, int32_t dtype, float scale, void *workspace,
+                    int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VAFA_H_ */

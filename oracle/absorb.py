@@ -1,0 +1,147 @@
+"""Absorbed ragged target attention, numpy restatement (test oracle only).
+
+Math (ta/kernels.py:23-45, ta/interface.py:429-435):
+  u[t,h,:]  = (q_raw[t] @ W_Q[:,h,:]) @ W_K[:,h,:]^T          [T_q, H, D_KV]
+  S[t,h,j]  = scale * u[t,h,:] . X[j,:]       (j in the segment of t)
+  P         = softmax_j(S)
+  aX[t,h,:] = sum_j P[t,h,j] X[j,:]
+  O[t,h,:]  = aX[t,h,:] @ W_V[:,h,:]                            [T_q, H, D_H]
+
+Restates ta/test_smoke.py:188-229 (absorbed) and ta/test_smoke.py:111-147 /
+150-185 (explicit K = X W_K, V = X W_V) in fp32 (or float64) without the
+reference oracles' rounding of p to the input dtype.  Gradients are the
+closed forms (dAX = dO W_V^T, dP = dAX X^T, dS = P*(dP - rowsum(P*dP)),
+du = scale dS X, dX = scale dS^T u + P^T dAX, dW_V = aX^T dO); tests pin
+them against torch.autograd on a float64 restatement.
+
+LSE is ``[T_q, H]`` log2 domain (ta/kernels.py:18-21); empty-key segments
+give O=0, LSE=-inf.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+LOG2E = 1.4426950408889634
+
+
+def _segs(cu_q, cu_k):
+    cq = np.asarray(cu_q, dtype=np.int64)
+    ck = np.asarray(cu_k, dtype=np.int64)
+    for i in range(cq.size - 1):
+        yield int(cq[i]), int(cq[i + 1]), int(ck[i]), int(ck[i + 1])
+
+
+def project_u(q_raw, W_Q, W_K, dtype=np.float32):
+    """u = q_raw @ W_Q @ W_K^T per head (ta/interface.py:434-435)."""
+    q_raw = np.asarray(q_raw, dtype=dtype)
+    W_Q = np.asarray(W_Q, dtype=dtype)
+    W_K = np.asarray(W_K, dtype=dtype)
+    T, d_q = q_raw.shape
+    _, H, D_H = W_Q.shape
+    qp = (q_raw @ W_Q.reshape(d_q, H * D_H)).reshape(T, H, D_H)
+    return np.einsum("thd,khd->thk", qp, W_K)
+
+
+def forward(u, X, W_V, cu_q, cu_k, scale, dtype=np.float32, return_ax=False):
+    """Inner op: returns ``(O [T_q,H,D_H], lse [T_q,H])`` (and aX if asked)."""
+    u = np.asarray(u, dtype=dtype)
+    X = np.asarray(X, dtype=dtype)
+    W_V = np.asarray(W_V, dtype=dtype)
+    T_q, H, D_KV = u.shape
+    D_H = W_V.shape[2]
+    ax = np.zeros((T_q, H, D_KV), dtype=dtype)
+    lse = np.full((T_q, H), -np.inf, dtype=dtype)
+    for q0, q1, k0, k1 in _segs(cu_q, cu_k):
+        if q1 == q0 or k1 == k0:
+            continue
+        s = np.einsum("thf,jf->thj", u[q0:q1], X[k0:k1]) * dtype(scale)
+        m = s.max(axis=-1, keepdims=True)
+        e = np.exp(s - m)
+        l = e.sum(axis=-1, keepdims=True)
+        p = e / l
+        ax[q0:q1] = np.einsum("thj,jf->thf", p, X[k0:k1])
+        lse[q0:q1] = (m[..., 0] + np.log(l[..., 0])) * dtype(LOG2E)
+    O = np.einsum("thf,fhd->thd", ax, W_V).astype(dtype)
+    if return_ax:
+        return O, lse, ax
+    return O, lse
+
+
+def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
+    """Inner op backward: returns ``(du, dX, dW_V)``."""
+    u = np.asarray(u, dtype=dtype)
+    X = np.asarray(X, dtype=dtype)
+    W_V = np.asarray(W_V, dtype=dtype)
+    dO = np.asarray(dO, dtype=dtype)
+    sc = dtype(scale)
+    du = np.zeros_like(u)
+    dX = np.zeros_like(X)
+    dW_V = np.zeros_like(W_V)
+    dax_all = np.einsum("thd,fhd->thf", dO, W_V)
+    for q0, q1, k0, k1 in _segs(cu_q, cu_k):
+        if q1 == q0 or k1 == k0:
+            continue
+        xs = X[k0:k1]
+        s = np.einsum("thf,jf->thj", u[q0:q1], xs) * sc
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)                     # [Lq, H, Lk]
+        ax = np.einsum("thj,jf->thf", p, xs)
+        dax = dax_all[q0:q1]
+        dp = np.einsum("thf,jf->thj", dax, xs)
+        ds = p * (dp - (p * dp).sum(axis=-1, keepdims=True))
+        du[q0:q1] = np.einsum("thj,jf->thf", ds, xs) * sc
+        dX[k0:k1] = (np.einsum("thj,thf->jf", ds, u[q0:q1]) * sc
+                     + np.einsum("thj,thf->jf", p, dax))
+        dW_V += np.einsum("thf,thd->fhd", ax, dO[q0:q1])
+    return du, dX, dW_V
+
+
+def full_forward(q_raw, X, W_Q, W_K, W_V, cu_q, cu_k, scale, dtype=np.float32):
+    """``packed_target_attn`` forward: O [T_q, H, D_H]."""
+    u = project_u(q_raw, W_Q, W_K, dtype)
+    return forward(u, X, W_V, cu_q, cu_k, scale, dtype)[0]
+
+
+def full_backward(q_raw, X, W_Q, W_K, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
+    """Grads of ``packed_target_attn`` w.r.t. (q_raw, X, W_Q, W_K, W_V).
+
+    The u-projection gradients follow the chain rule through
+    ta/interface.py:434-435.
+    """
+    q_raw = np.asarray(q_raw, dtype=dtype)
+    W_Q = np.asarray(W_Q, dtype=dtype)
+    W_K = np.asarray(W_K, dtype=dtype)
+    T, d_q = q_raw.shape
+    _, H, D_H = W_Q.shape
+    qp = (q_raw @ W_Q.reshape(d_q, H * D_H)).reshape(T, H, D_H)
+    u = np.einsum("thd,khd->thk", qp, W_K)
+    du, dX, dW_V = backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype)
+    dqp = np.einsum("thk,khd->thd", du, W_K)
+    dW_K = np.einsum("thk,thd->khd", du, qp)
+    dq_raw = dqp.reshape(T, H * D_H) @ W_Q.reshape(d_q, H * D_H).T
+    dW_Q = (q_raw.T @ dqp.reshape(T, H * D_H)).reshape(d_q, H, D_H)
+    return dq_raw, dX, dW_Q, dW_K, dW_V
+
+
+def explicit_forward(q_raw, X, W_Q, W_K, W_V, cu_q, cu_k, scale, dtype=np.float64):
+    """Explicit K = X W_K, V = X W_V per head (ta/test_smoke.py:111-147)."""
+    q_raw = np.asarray(q_raw, dtype=dtype)
+    X = np.asarray(X, dtype=dtype)
+    W_Q, W_K, W_V = (np.asarray(w, dtype=dtype) for w in (W_Q, W_K, W_V))
+    T_q = q_raw.shape[0]
+    _, H, D_H = W_Q.shape
+    O = np.zeros((T_q, H, D_H), dtype=dtype)
+    for q0, q1, k0, k1 in _segs(cu_q, cu_k):
+        if q1 == q0 or k1 == k0:
+            continue
+        for h in range(H):
+            qp = q_raw[q0:q1] @ W_Q[:, h, :]
+            kp = X[k0:k1] @ W_K[:, h, :]
+            vp = X[k0:k1] @ W_V[:, h, :]
+            s = qp @ kp.T * scale
+            s -= s.max(axis=-1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=-1, keepdims=True)
+            O[q0:q1, h, :] = p @ vp
+    return O

@@ -1,0 +1,137 @@
+"""GPU parity of packed_target_attn against the CPU oracle.
+
+Cases follow ta/test_smoke.py:2295-2338 (d_q=968, d_kv=216, H=8, D_H=32,
+inputs randn*0.1 as in ta/test_smoke.py:373-395); all five outputs are
+compared (O and the grads of q_raw, X, W_Q, W_K, W_V).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import absorb as oa
+from parity import assert_close
+from varlenabsorbflashattn_amd import (packed_target_attn, prepare_target_attn_indices,
+                                       target_attn_inner)
+from varlenabsorbflashattn_amd.workloads import cu_from_lens
+
+pytestmark = pytest.mark.gpu
+
+FP32_CASES = [
+    ("smoke", [4], [64]),
+    ("single_segment", [7], [256]),
+    ("4_uniform", [8, 8, 8, 8], [256] * 4),
+    ("4_ragged_real", [7, 8, 6, 9], [2048, 1024, 1536, 512]),
+    ("k_tail", [5, 7, 9], [123, 257, 999]),
+    ("q_tail", [33, 65, 129], [256, 256, 256]),
+    ("short_k_ragged", [1, 2, 4, 8], [1, 3, 7, 15]),
+    ("mixed_block_tails", [15, 16, 17, 31], [31, 32, 33, 65]),
+    ("nq1_mini", [1], [512]),
+]
+BF16_CASES = [FP32_CASES[i] for i in (0, 3, 4, 5, 6, 7, 8)] + [
+    ("long_split", [3, 40], [5000, 9000]),
+    ("empty_q", [0, 5, 0], [7, 20, 0]),
+]
+
+
+def make_inputs(q_lens, k_lens, d_q=968, d_kv=216, H=8, D_H=32, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    T_q, T_k = sum(q_lens), sum(k_lens)
+    q_raw = torch.randn(T_q, d_q, generator=g) * 0.1
+    X = torch.randn(T_k, d_kv, generator=g) * 0.1
+    W_Q = torch.randn(d_q, H, D_H, generator=g) * 0.1
+    W_K = torch.randn(d_kv, H, D_H, generator=g) * 0.1
+    W_V = torch.randn(d_kv, H, D_H, generator=g) * 0.1
+    return q_raw, X, W_Q, W_K, W_V
+
+
+def run_case(q_lens, k_lens, dtype, device, **kw):
+    ins = make_inputs(q_lens, k_lens, **kw)
+    ins = [t.to(dtype) for t in ins]
+    cq, ck = cu_from_lens(q_lens), cu_from_lens(k_lens)
+    dev = [t.to(device).requires_grad_(True) for t in ins]
+    O = packed_target_attn(*dev, cu_seqlens_q=cq.to(device), cu_seqlens_k=ck.to(device))
+    g = torch.Generator().manual_seed(7)
+    dO = (torch.randn(O.shape, generator=g) * 0.1).to(dtype)
+    O.backward(dO.to(device))
+    torch.cuda.synchronize()
+    D_H = ins[2].shape[2]
+    scale = 1.0 / math.sqrt(D_H)
+    npy = [t.float().numpy() for t in ins]
+    O_ref = oa.full_forward(*npy, cq.numpy(), ck.numpy(), scale, np.float64)
+    grads = oa.full_backward(*npy, dO.float().numpy(), cq.numpy(), ck.numpy(), scale, np.float64)
+    return [O] + [t.grad for t in dev], [O_ref] + list(grads)
+
+
+NAMES = ("O", "dq_raw", "dX", "dW_Q", "dW_K", "dW_V")
+
+
+@pytest.mark.parametrize("name,q_lens,k_lens", FP32_CASES, ids=[c[0] for c in FP32_CASES])
+def test_absorb_fp32_parity(device, name, q_lens, k_lens):
+    print(f"[absorb fp32] {name}", flush=True)
+    got, ref = run_case(q_lens, k_lens, torch.float32, device)
+    for n, a, r in zip(NAMES, got, ref):
+        assert_close(n, a, r)
+
+
+@pytest.mark.parametrize("name,q_lens,k_lens", BF16_CASES, ids=[c[0] for c in BF16_CASES])
+def test_absorb_bf16_parity(device, name, q_lens, k_lens):
+    print(f"[absorb bf16] {name}", flush=True)
+    got, ref = run_case(q_lens, k_lens, torch.bfloat16, device)
+    for n, a, r in zip(NAMES, got, ref):
+        assert_close(n, a, r)
+
+
+def test_absorb_bf16_config4_dims(device):
+    """C4 dims (D_in=256, N(0,1) inputs, Xavier weights) on a small sample."""
+    from varlenabsorbflashattn_amd import workloads as W
+    case = W.config4(seed=3, n=24)
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, "cpu")
+    cq, ck = cu_from_lens(case.q_lens), cu_from_lens(case.k_lens)
+    scale = 1.0 / math.sqrt(case.D_H)
+    u = oa.project_u(*(t.float().numpy() for t in (q_raw, W_Q, W_K)), dtype=np.float64)
+    u_t = torch.from_numpy(u).to(torch.bfloat16)
+    O = target_attn_inner(u_t.to(device), X.to(device), W_V.to(device), cq.to(device),
+                          ck.to(device), scale)
+    O_ref, _ = oa.forward(u_t.float().numpy(), X.float().numpy(), W_V.float().numpy(),
+                          cq.numpy(), ck.numpy(), scale, np.float64)
+    assert_close("O", O, O_ref)
+
+
+def test_prepared_indices_fast_path(device):
+    q_lens, k_lens = [7, 8, 6, 9], [2048, 1024, 1536, 512]
+    ins = [t.to(device, torch.bfloat16) for t in make_inputs(q_lens, k_lens)]
+    cq, ck = cu_from_lens(q_lens).to(device), cu_from_lens(k_lens).to(device)
+    qi, ki = prepare_target_attn_indices(cq, ck)
+    from oracle import meta
+    assert np.array_equal(qi.cpu().numpy(), meta.chunk_indices(cq.cpu().numpy(), 16))
+    assert np.array_equal(ki.cpu().numpy(), meta.chunk_indices(ck.cpu().numpy(), 64))
+    a = packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    b = packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck, q_chunk_indices=qi,
+                           k_chunk_indices=ki, validate=False)
+    assert torch.equal(a, b)
+
+
+def test_absorb_deterministic(device):
+    q_lens, k_lens = [5, 7, 9, 30], [123, 257, 999, 3000]
+    outs = []
+    for _ in range(2):
+        ins = [t.to(device, torch.bfloat16).requires_grad_(True)
+               for t in make_inputs(q_lens, k_lens)]
+        O = packed_target_attn(*ins, cu_seqlens_q=cu_from_lens(q_lens).to(device),
+                               cu_seqlens_k=cu_from_lens(k_lens).to(device))
+        O.backward(torch.ones_like(O))
+        outs.append([O.detach()] + [t.grad for t in ins])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_absorb_validation_errors(device):
+    ins = [t.to(device) for t in make_inputs([2, 3], [4, 5])]
+    with pytest.raises(ValueError, match="k_len > 0"):
+        packed_target_attn(*ins, cu_seqlens_q=torch.tensor([0, 2, 5], device=device),
+                           cu_seqlens_k=torch.tensor([0, 9, 9], device=device))
+    with pytest.raises(ValueError):
+        packed_target_attn(*ins, cu_seqlens_q=torch.tensor([0, 2, 6], device=device),
+                           cu_seqlens_k=torch.tensor([0, 4, 9], device=device))

@@ -1,0 +1,196 @@
+"""GPU parity of packed_varlen_attn against the CPU oracle.
+
+Cases follow fa/test_smoke.py:217-351 (bf16, H=4, D=64 unless noted); the
+invariants follow fa/test_smoke.py:354-531.  Tolerances: see tests/parity.py.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import varlen as ov
+from parity import assert_close
+from varlenabsorbflashattn_amd import packed_varlen_attn, set_validate_cu_seqlens
+from varlenabsorbflashattn_amd.workloads import cu_from_lens
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ("tiny", [7, 11], [19, 5], 64),
+    ("cross_block", [129, 257], [33, 130], 64),
+    ("stage1_like", [500, 500], [19, 800], 64),
+    ("stage2_like", [512, 512], [500, 500], 64),
+    ("single_seg", [400], [400], 64),
+    ("block_aligned", [256, 256], [128, 128], 64),
+    ("head_dim_128", [200, 300], [150, 250], 128),
+    ("head_dim_32", [70, 5], [90, 200], 32),
+    ("head_dim_256", [130, 3], [77, 300], 256),
+    ("head_dim_16", [33, 9], [40, 70], 16),
+    ("empty_segments", [0, 5, 9, 0], [3, 0, 40, 7], 64),
+    ("long_split", [150, 20], [9000, 5000], 64),
+    ("decode_split", [3, 16, 1], [3000, 1500, 1024], 128),
+]
+
+
+def run_case(q_lens, k_lens, H, D, dtype, device, seed=0, dist_scale=1.0):
+    torch.manual_seed(seed)
+    Tq, Tk = sum(q_lens), sum(k_lens)
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(Tq, H, D, generator=g) * dist_scale).to(dtype)
+    k = (torch.randn(Tk, H, D, generator=g) * dist_scale).to(dtype)
+    v = torch.randn(Tk, H, D, generator=g).to(dtype)
+    do = torch.randn(Tq, H, D, generator=g).to(dtype)
+    cq, ck = cu_from_lens(q_lens), cu_from_lens(k_lens)
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = packed_varlen_attn(qd, kd, vd, cu_seqlens_q=cq.to(device), cu_seqlens_k=ck.to(device),
+                           scale=scale)
+    o.backward(do.to(device))
+    torch.cuda.synchronize()
+    f64 = np.float64
+    o_ref, _ = ov.forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), cq.numpy(),
+                          ck.numpy(), scale, f64)
+    dq_r, dk_r, dv_r = ov.backward(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                   do.float().numpy(), cq.numpy(), ck.numpy(), scale, f64)
+    return (o, qd.grad, kd.grad, vd.grad), (o_ref, dq_r, dk_r, dv_r)
+
+
+@pytest.mark.parametrize("name,q_lens,k_lens,D", CASES, ids=[c[0] for c in CASES])
+def test_varlen_bf16_parity(device, name, q_lens, k_lens, D):
+    print(f"[varlen bf16] {name} q={q_lens} k={k_lens} D={D}", flush=True)
+    got, ref = run_case(q_lens, k_lens, 4, D, torch.bfloat16, device)
+    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(n, a, r)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+def test_varlen_other_dtypes(device, dtype):
+    print(f"[varlen {dtype}]", flush=True)
+    got, ref = run_case([17, 64, 128, 200], [17, 64, 128, 200], 4, 64, dtype, device)
+    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(n, a, r)
+
+
+def test_varlen_config1_fp32(device):
+    """fp32, lens {17,64,128,200}, H=4, D=64 (N(0,1) inputs)."""
+    got, ref = run_case([17, 64, 128, 200], [17, 64, 128, 200], 4, 64, torch.float32, device,
+                        seed=1)
+    assert_close("o", got[0], ref[0])
+
+
+@pytest.mark.parametrize("dist", [8.0, 0.05])
+def test_varlen_input_scales(device, dist):
+    """Stress distributions of fa-tools/benchmark_packed_varlen_flash_attn.py:226-233."""
+    got, ref = run_case([100, 37], [300, 64], 4, 64, torch.bfloat16, device, dist_scale=dist)
+    assert_close("o", got[0], ref[0])
+
+
+def test_single_key_returns_v(device):
+    """Lk = 1: softmax weight 1 -> O == V exactly; dq = dk = 0."""
+    H, D = 2, 64
+    q = torch.randn(5, H, D, device=device, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.randn(1, H, D, device=device, dtype=torch.bfloat16, requires_grad=True)
+    v = torch.randn(1, H, D, device=device, dtype=torch.bfloat16, requires_grad=True)
+    o = packed_varlen_attn(q, k, v, cu_seqlens_q=torch.tensor([0, 5], device=device),
+                           cu_seqlens_k=torch.tensor([0, 1], device=device))
+    assert torch.equal(o, v.expand(5, H, D))
+    o.backward(torch.randn_like(o))
+    assert q.grad.abs().max().item() == 0.0 and k.grad.abs().max().item() == 0.0
+
+
+def test_one_hot_segment_values(device):
+    """V one-hot on the segment id: column seg is ~1, every other column exactly 0."""
+    lens = [3, 70, 129, 1, 260]
+    H, D = 2, 64
+    cu = cu_from_lens(lens).to(device)
+    T = sum(lens)
+    seg = torch.repeat_interleave(torch.arange(len(lens)), torch.tensor(lens))
+    v = torch.zeros(T, H, D)
+    v[torch.arange(T), :, seg] = 1.0
+    q = torch.randn(T, H, D)
+    k = torch.randn(T, H, D)
+    o = packed_varlen_attn(*(t.to(device, torch.bfloat16) for t in (q, k, v)),
+                           cu_seqlens_q=cu, cu_seqlens_k=cu).float().cpu()
+    mask = torch.zeros(T, H, D, dtype=torch.bool)
+    mask[torch.arange(T), :, seg] = True
+    assert o[~mask].abs().max().item() == 0.0
+    assert (o[mask] - 1).abs().max().item() < 1e-2
+
+
+def _inputs(device, q_lens=(129, 257), k_lens=(33, 130), H=4, D=64, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    Tq, Tk = sum(q_lens), sum(k_lens)
+    q, k, v = (torch.randn(T, H, D, generator=g).to(device, torch.bfloat16)
+               for T in (Tq, Tk, Tk))
+    return q, k, v, cu_from_lens(q_lens).to(device), cu_from_lens(k_lens).to(device)
+
+
+def test_no_grad_equals_grad(device):
+    q, k, v, cq, ck = _inputs(device)
+    with torch.no_grad():
+        a = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    b = packed_varlen_attn(q.requires_grad_(), k.requires_grad_(), v.requires_grad_(),
+                           cu_seqlens_q=cq, cu_seqlens_k=ck)
+    assert torch.equal(a, b.detach())
+
+
+def test_3d_equals_4d(device):
+    q, k, v, cq, ck = _inputs(device)
+    outs = []
+    for unsq in (False, True):
+        qq, kk, vv = (t.detach().clone().unsqueeze(0) if unsq else t.detach().clone()
+                      for t in (q, k, v))
+        for t in (qq, kk, vv):
+            t.requires_grad_(True)
+        o = packed_varlen_attn(qq, kk, vv, cu_seqlens_q=cq, cu_seqlens_k=ck)
+        assert o.dim() == (4 if unsq else 3)
+        o.backward(torch.ones_like(o))
+        outs.append([t.squeeze(0) for t in (o.detach(), qq.grad, kk.grad, vv.grad)])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_repeatable_bit_exact(device):
+    """Two runs with dO = 1 agree bit for bit (no atomics; fa/test_smoke.py:496-531)."""
+    q, k, v, cq, ck = _inputs(device, q_lens=(300, 20), k_lens=(9000, 500))
+    res = []
+    for _ in range(2):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = packed_varlen_attn(qq, kk, vv, cu_seqlens_q=cq, cu_seqlens_k=ck)
+        o.backward(torch.ones_like(o))
+        res.append((o.detach(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_partial_grad(device):
+    """Only q requires grad: k.grad / v.grad stay None (fa/test_smoke.py:379-407)."""
+    q, k, v, cq, ck = _inputs(device)
+    q.requires_grad_(True)
+    o = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    o.sum().backward()
+    assert q.grad is not None and k.grad is None and v.grad is None
+
+
+def test_seqinfo_equals_cu_and_validation_toggle(device):
+    q, k, v, cq, ck = _inputs(device)
+    a = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    b = packed_varlen_attn(q, k, v, q_seqinfo=torch.tensor([129, 257], device=device),
+                           k_seqinfo=torch.tensor([33, 130], device=device))
+    set_validate_cu_seqlens(False)
+    try:
+        c = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    finally:
+        set_validate_cu_seqlens(True)
+    assert torch.equal(a, b) and torch.equal(a, c)
+    with pytest.raises(ValueError):
+        packed_varlen_attn(q, k, v, cu_seqlens_q=torch.tensor([0, 100, 380], device=device),
+                           cu_seqlens_k=ck)
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_multi_seed(device, seed):
+    got, ref = run_case([77, 200, 3], [150, 31, 260], 4, 64, torch.bfloat16, device, seed=seed)
+    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(n, a, r)

@@ -1,0 +1,228 @@
+"""Host metadata and work plans (CPU): bit-exact against the oracle, plus
+coverage invariants checked by brute force."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from oracle import meta
+from varlenabsorbflashattn_amd import _lib
+
+GOLD = os.path.join(ROOT, "tests", "golden")
+
+
+def _cu(lens):
+    c = np.zeros(len(lens) + 1, dtype=np.int64)
+    c[1:] = np.cumsum(lens)
+    return c
+
+
+def _stage1_cases():
+    with open(os.path.join(GOLD, "stage1_shapes_subset.jsonl")) as f:
+        return [json.loads(l) for l in f if l.strip()]
+
+
+# ---- oracle pins -------------------------------------------------------------
+
+def test_oracle_chunk_indices_brute_force():
+    rng = np.random.default_rng(1)
+    for _ in range(50):
+        lens = rng.integers(0, 300, size=rng.integers(1, 12))
+        bt = int(rng.choice([1, 16, 64, 128]))
+        want = [(s, b) for s, L in enumerate(lens) for b in range(-(-int(L) // bt))]
+        got = meta.chunk_indices(_cu(lens), bt)
+        assert got.tolist() == [list(x) for x in want]
+
+
+def test_oracle_seqinfo_matches_cumsum_and_errors():
+    assert meta.seqinfo_to_cu([3, 0, 5]).tolist() == [0, 3, 3, 8]
+    with pytest.raises(ValueError):
+        meta.seqinfo_to_cu([])
+    with pytest.raises(ValueError):
+        meta.seqinfo_to_cu([1, -1])
+    with pytest.raises(ValueError):
+        meta.seqinfo_to_cu([[1, 2]])
+    with pytest.raises(ValueError):
+        meta.seqinfo_to_cu([2**31 - 1, 1])
+
+
+def test_oracle_split_plan_reference_example():
+    # Lk = 9000 > 4096 -> 3 slices of 4096; q block of 128 rows: 2 blocks for Lq=200
+    short, split, comb = meta.split_plan(_cu([10, 200]), _cu([50, 9000]), 128, 4096, 4096)
+    assert short.tolist() == [[0, 0]]
+    assert split.tolist() == [[1, 0, 0], [1, 0, 1], [1, 0, 2], [1, 1, 0], [1, 1, 1], [1, 1, 2]]
+    assert comb.tolist() == [[1, 0, 0, 3], [1, 1, 3, 3]]
+
+
+# ---- product vs oracle (bit-exact) --------------------------------------------
+
+@pytest.mark.parametrize("seed", range(8))
+def test_seqinfo_to_cu_bit_exact(seed):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 5000, size=rng.integers(1, 200))
+    assert np.array_equal(_lib.seqinfo_to_cu(lens), meta.seqinfo_to_cu(lens))
+
+
+@pytest.mark.parametrize("bad", [[], [1, -2, 3], [2**31 - 1, 5]])
+def test_seqinfo_to_cu_errors_match(bad):
+    with pytest.raises(ValueError) as e_ref:
+        meta.seqinfo_to_cu(bad)
+    with pytest.raises(ValueError) as e_new:
+        _lib.seqinfo_to_cu(np.asarray(bad, dtype=np.int64))
+    assert str(e_ref.value).split()[0] == str(e_new.value).split()[0]
+
+
+@pytest.mark.parametrize("cu,T", [([0, 3, 5], 5), ([1, 3, 5], 5), ([0, 3, 4], 5),
+                                  ([0, 4, 3, 5], 5), ([0], 0)])
+def test_validate_cu_matches_oracle(cu, T):
+    ref_err = new_err = None
+    try:
+        meta.validate_cu_seqlens(np.array(cu), T, "cu_seqlens_q")
+    except ValueError as e:
+        ref_err = str(e)
+    try:
+        _lib.validate_cu(np.array(cu), T, "cu_seqlens_q")
+    except ValueError as e:
+        new_err = str(e)
+    assert ref_err == new_err
+
+
+def test_active_segments_have_keys():
+    _lib.check_active_have_keys(np.array([0, 2, 2]), np.array([0, 5, 5]))
+    with pytest.raises(ValueError, match="k_len > 0"):
+        _lib.check_active_have_keys(np.array([0, 2, 3]), np.array([0, 5, 5]))
+
+
+@pytest.mark.parametrize("bt", [16, 64, 128])
+def test_chunk_indices_bit_exact(bt):
+    rng = np.random.default_rng(bt)
+    for _ in range(20):
+        lens = rng.integers(0, 700, size=rng.integers(1, 40))
+        assert np.array_equal(_lib.chunk_indices(_cu(lens), bt), meta.chunk_indices(_cu(lens), bt))
+
+
+def test_chunk_indices_real_shapes():
+    rec = json.load(open(os.path.join(GOLD, "ta_real_shape_subset.json")))["records"][0]
+    for lens, bt in ((rec["q_lens"], 16), (rec["k_lens"], 64)):
+        assert np.array_equal(_lib.chunk_indices(_cu(lens), bt), meta.chunk_indices(_cu(lens), bt))
+
+
+# ---- plan invariants ------------------------------------------------------------
+
+def check_varlen_plan(q_lens, k_lens, H=4, D=64):
+    cq, ck = _cu(q_lens), _cu(k_lens)
+    p = _lib.plan_varlen(cq, ck, H, D)
+    fwd, comb, kv = p.section("fwd"), p.section("comb"), p.section("kv")
+    BM = p.info.q_tile
+    # 1) every (query row, key) pair of a segment is covered by exactly one item
+    cover = {}
+    for q0, q1, k0, k1, pb, seg, s, ns in fwd.tolist():
+        assert cq[seg] <= q0 < q1 <= cq[seg + 1] and q1 - q0 <= BM
+        assert ck[seg] <= k0 <= k1 <= ck[seg + 1]
+        assert (q0 - cq[seg]) % BM == 0
+        cover.setdefault((q0, q1), []).append((k0, k1, pb, s, ns))
+    for seg in range(len(q_lens)):
+        for t in range(cq[seg], cq[seg + 1], BM):
+            ranges = sorted(cover.pop((t, min(t + BM, cq[seg + 1]))))
+            # key slices partition [ck[seg], ck[seg+1])
+            assert ranges[0][0] == ck[seg] and ranges[-1][1] == ck[seg + 1]
+            for a, b in zip(ranges, ranges[1:]):
+                assert a[1] == b[0]
+            ns = len(ranges)
+            assert all(r[4] == ns for r in ranges)
+            assert (ranges[0][2] == -1) == (ns == 1)
+    assert not cover
+    # 2) split partial rows are disjoint, contiguous per tile, inside n_part_rows
+    used = np.zeros(p.info.n_part_rows, dtype=np.int64)
+    for q0, q1, pbase, ns, seg, *_ in comb.tolist():
+        R = q1 - q0
+        slots = sorted((r[4], r[6]) for r in fwd.tolist() if r[0] == q0 and r[1] == q1)
+        assert [s for _, s in slots] == list(range(ns))
+        assert [b for b, _ in slots] == [pbase + s * R for s in range(ns)]
+        used[pbase:pbase + ns * R] += 1
+    assert (used == 1).all()
+    # 3) key tiles cover each key once and carry the segment's query range
+    keys = np.zeros(int(ck[-1]), dtype=np.int64)
+    for k0, k1, q0, q1, seg, *_ in kv.tolist():
+        assert (q0, q1) == (cq[seg], cq[seg + 1])
+        keys[k0:k1] += 1
+    assert (keys == 1).all()
+    # 4) longest-first order
+    lens = (fwd[:, 3] - fwd[:, 2]).astype(np.int64)
+    assert (np.diff(lens) <= 0).all()
+    return p
+
+
+def test_varlen_plan_small_cases():
+    cases = [([7, 11], [19, 5]), ([129, 257], [33, 130]), ([500, 500], [19, 800]),
+             ([512, 512], [500, 500]), ([400], [400]), ([256, 256], [128, 128]),
+             ([0, 5, 0], [3, 0, 9]), ([300, 20], [9000, 70000]), ([16, 3], [32768, 1024])]
+    for ql, kl in cases:
+        check_varlen_plan(ql, kl)
+
+
+def test_varlen_plan_split_counts_match_reference_rule():
+    # prefill-like tiles split ceil(Lk/4096) ways like fa/chunk_indices.py:172-287
+    ql, kl = [300, 200, 40], [9000, 4096, 70000]
+    p = check_varlen_plan(ql, kl)
+    _, split, comb = meta.split_plan(_cu(ql), _cu(kl), 128, 4096, 4096)
+    assert p.info.n_comb == comb.shape[0]
+    assert p.info.n_fwd - (3 + 2 + 1 - comb.shape[0]) == split.shape[0]
+
+
+def test_varlen_plan_decode_split_range():
+    # Lq <= 16 against >= 1024 keys: 4..16 key chunks per tile
+    rng = np.random.default_rng(0)
+    lq = rng.integers(1, 17, size=64).tolist()
+    lk = rng.integers(1024, 32769, size=64).tolist()
+    p = check_varlen_plan(lq, lk, H=32, D=128)
+    ns = p.section("comb")[:, 3]
+    assert ns.min() >= 4 and ns.max() <= 16 and len(ns) == 64
+
+
+def test_varlen_plan_stage1_shapes():
+    for row in _stage1_cases()[:3]:
+        check_varlen_plan(row["q_lens"], row["k_lens"])
+
+
+def check_absorb_plan(q_lens, k_lens, H=8):
+    cq, ck = _cu(q_lens), _cu(k_lens)
+    p = _lib.plan_absorb(cq, ck, H, 256, 32)
+    TT = p.info.q_tile
+    assert TT * H <= 128
+    cover = {}
+    for t0, t1, k0, k1, pb, seg, s, ns in p.section("fwd").tolist():
+        assert cq[seg] <= t0 < t1 <= cq[seg + 1] and t1 - t0 <= TT
+        cover.setdefault((t0, t1), []).append((k0, k1))
+    qt = p.section("qt")
+    n_tiles = sum(-(-int(L) // TT) for L in q_lens)
+    assert len(qt) == n_tiles == len(cover)
+    for t0, t1, k0, k1, pb, seg, *_ in qt.tolist():
+        r = sorted(cover[(t0, t1)])
+        assert r[0][0] == k0 == ck[seg] and r[-1][1] == k1 == ck[seg + 1]
+    keys = np.zeros(int(ck[-1]), dtype=np.int64)
+    for k0, k1, t0, t1, seg, *_ in p.section("kv").tolist():
+        keys[k0:k1] += 1
+        assert (t0, t1) == (cq[seg], cq[seg + 1])
+    assert (keys == 1).all()
+    return p
+
+
+def test_absorb_plan_cases():
+    for ql, kl in [([4], [64]), ([7, 8, 6, 9], [2048, 1024, 1536, 512]), ([5, 7, 9], [123, 257, 999]),
+                   ([33, 65, 129], [256] * 3), ([1, 2, 4, 8], [1, 3, 7, 15]), ([0, 3], [5, 0])]:
+        check_absorb_plan(ql, kl)
+
+
+def test_absorb_plan_real_shapes():
+    rec = json.load(open(os.path.join(GOLD, "ta_real_shape_subset.json")))["records"][1]
+    check_absorb_plan(rec["q_lens"], rec["k_lens"])
+
+
+def test_plan_rejects_bad_cu():
+    with pytest.raises(ValueError):
+        _lib.plan_varlen(np.array([0, 5, 3]), np.array([0, 1, 2]), 2, 64)
+    with pytest.raises(AssertionError):
+        _lib.plan_varlen(np.array([0, 5]), np.array([0, 1, 2]), 2, 64)

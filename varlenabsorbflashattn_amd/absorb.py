@@ -1,0 +1,288 @@
+"""Ragged absorbed target attention -- drop-in for
+``triton_target_attn_absorb`` (ta/interface.py:125-454).
+
+``packed_target_attn`` keeps the reference signature: it projects
+``u = q_raw W_Q W_K^T`` per head with plain library GEMMs (autograd carries
+dq_raw / dW_Q / dW_K, as in ta/interface.py:429-435) and calls
+``target_attn_inner``, whose forward and backward run in ``libvafa.so``:
+scores are taken directly against the raw ``X`` rows, ``aX = softmax(u X^T) X``
+is accumulated on the fly and projected by ``W_V`` at the end.  The backward
+is deterministic (dW_V and dX are reduced in a fixed order).
+"""
+from __future__ import annotations
+
+import math
+import os
+import weakref
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+
+# Reference block sizes, kept for the (seg, block) tables that
+# prepare_target_attn_indices returns (ta/interface.py:59-63).
+_BT_Q_FWD = 16
+_BT_K_BWD = 64
+
+# prepare_target_attn_indices() remembers the host cu_seqlens behind the
+# tables it returns, so a later validate=False call needs no device->host copy.
+# Keyed by id() with a weak reference to the table (tensors compare by value).
+_HOST_CU: dict = {}
+
+
+def _remember_host_cu(table: torch.Tensor, cu_q_h: np.ndarray, cu_k_h: np.ndarray) -> None:
+    key = id(table)
+    _HOST_CU[key] = (weakref.ref(table, lambda _r, k=key: _HOST_CU.pop(k, None)), cu_q_h, cu_k_h)
+
+
+def _recall_host_cu(table: Optional[torch.Tensor]):
+    if table is None:
+        return None
+    hit = _HOST_CU.get(id(table))
+    if hit is None or hit[0]() is not table:
+        return None
+    return hit[1], hit[2]
+
+
+def _select_fwd_mode() -> str:
+    """TRITON_TARGET_ATTN_FWD_MODE as in ta/interface.py:66-70.
+
+    Both accepted modes run the same fused kernel here; the variable keeps
+    its validation so existing configurations behave the same.
+    """
+    mode = os.environ.get("TRITON_TARGET_ATTN_FWD_MODE", "alpha").lower()
+    if mode in ("direct", "alpha"):
+        return mode
+    raise ValueError("TRITON_TARGET_ATTN_FWD_MODE must be one of: direct, alpha")
+
+
+def _select_dx_mode(n_k_chunks: int) -> str:
+    """TRITON_TARGET_ATTN_DX_MODE as in ta/interface.py:73-85 (validation only:
+    every mode maps to the deterministic dX kernel)."""
+    mode = os.environ.get("TRITON_TARGET_ATTN_DX_MODE", "auto").lower()
+    if mode in ("partial", "fused", "atomic"):
+        return mode
+    if mode != "auto":
+        raise ValueError(
+            "TRITON_TARGET_ATTN_DX_MODE must be one of: auto, partial, fused, atomic")
+    return "fused" if n_k_chunks >= 1024 else "partial"
+
+
+def _validate_cu_seqlens(cu_host: np.ndarray, shape, T: int, name: str) -> None:
+    """ta/interface.py:92-106."""
+    if len(shape) != 1 or cu_host.size < 2:
+        raise ValueError(f"{name}: must be 1-D with len>=2, got {tuple(shape)}")
+    _lib.validate_cu(cu_host, T, name)
+
+
+def _next_power_of_2(x: int) -> int:
+    if x < 1:
+        raise ValueError(f"expected positive dimension, got {x}")
+    return 1 << (x - 1).bit_length()
+
+
+def prepare_target_attn_indices(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor):
+    """Chunk tables ``(q_idx [NT_q,2], k_idx [NT_k,2])`` (ta/interface.py:125-138).
+
+    Same content as the reference (BT_Q=16, BT_K=64 rows ``(seg, block)``).
+    Passing them back with ``validate=False`` skips every host round trip:
+    the host cu_seqlens captured here are reused to look up the cached plan.
+    """
+    cu_q_h = _lib.as_host_i64(cu_seqlens_q)
+    cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+    q_idx = torch.from_numpy(_lib.chunk_indices(cu_q_h, _BT_Q_FWD)).to(cu_seqlens_q.device)
+    k_idx = torch.from_numpy(_lib.chunk_indices(cu_k_h, _BT_K_BWD)).to(cu_seqlens_k.device)
+    _remember_host_cu(q_idx, cu_q_h, cu_k_h)
+    return q_idx, k_idx
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 0), dtype=torch.uint8, device=device)
+
+
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    return x.clone() if x.data_ptr() % 16 != 0 else x
+
+
+class _TargetAttnFunction(torch.autograd.Function):
+    """Inner op on projected u (ta/interface.py:141-321)."""
+
+    @staticmethod
+    def forward(ctx, u, X, W_V, cu_seqlens_q, cu_seqlens_k, scale, q_chunk_indices,
+                k_chunk_indices, validate):
+        T_q, H, D_KV = u.shape
+        T_k, D_KV_x = X.shape
+        D_KV_wv, H_wv, D_H = W_V.shape
+        assert D_KV == D_KV_x == D_KV_wv, \
+            f"D_KV mismatch: u={D_KV}, X={D_KV_x}, W_V={D_KV_wv}"
+        assert H == H_wv, f"H mismatch: u={H}, W_V={H_wv}"
+        assert u.dtype == X.dtype == W_V.dtype, \
+            f"u/X/W_V must share dtype, got {u.dtype}/{X.dtype}/{W_V.dtype}"
+        assert u.is_cuda and X.is_cuda and W_V.is_cuda, "all inputs must be GPU tensors"
+        assert u.device == X.device == W_V.device, "u/X/W_V must be on same device"
+        assert D_H in (16, 32, 64, 128, 256), f"D_H {D_H} not supported"
+        dcode = _lib.dtype_code(u.dtype)
+
+        known = _recall_host_cu(q_chunk_indices)
+        if known is not None and not validate:
+            cu_q_h, cu_k_h = known
+        else:
+            cu_q_h = _lib.as_host_i64(cu_seqlens_q)
+            cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+        if validate:
+            n_seg = cu_seqlens_q.numel() - 1
+            assert cu_seqlens_k.numel() - 1 == n_seg, "segment count mismatch q vs k"
+            _validate_cu_seqlens(cu_q_h, cu_seqlens_q.shape, T_q, "cu_seqlens_q")
+            _validate_cu_seqlens(cu_k_h, cu_seqlens_k.shape, T_k, "cu_seqlens_k")
+            _lib.check_active_have_keys(cu_q_h, cu_k_h)
+
+        u, X, W_V = (_aligned(t.contiguous()) for t in (u, X, W_V))
+        B_DKV = _next_power_of_2(D_KV)
+        assert B_DKV <= 512, f"D_KV={D_KV} pads to {B_DKV}, which is too large"
+
+        plan = _lib.device_plan("absorb", cu_q_h, cu_k_h, (H, D_KV, D_H), u.device)
+        if plan.info.T_q > T_q or plan.info.T_k > T_k:
+            raise ValueError(
+                f"cu_seqlens address {plan.info.T_q} query / {plan.info.T_k} key tokens but "
+                f"the inputs hold {T_q} / {T_k}")
+        O = torch.empty((T_q, H, D_H), dtype=u.dtype, device=u.device)
+        LSE = torch.empty((T_q, H), dtype=torch.float32, device=u.device)
+        if plan.info.n_fwd > 0:
+            _select_fwd_mode()
+        L = _lib.lib()
+        ws = _workspace(L.vafa_absorb_fwd_workspace(plan.info, D_KV, D_H), u.device)
+        _lib.check(L.vafa_absorb_fwd(
+            u.data_ptr(), X.data_ptr(), W_V.data_ptr(), O.data_ptr(), LSE.data_ptr(),
+            plan.items.data_ptr(), plan.info, D_KV, D_H, dcode, float(scale),
+            ws.data_ptr() if ws.numel() else None, ws.numel(), _lib.stream_ptr(u.device)))
+        ctx.save_for_backward(u, X, W_V, O, LSE)
+        ctx.plan = plan
+        ctx.scale = scale
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):
+        u, X, W_V, O, LSE = ctx.saved_tensors
+        plan = ctx.plan
+        T_q, H, D_KV = u.shape
+        D_H = W_V.shape[2]
+        if dO.stride(-1) != 1 or not dO.is_contiguous():
+            dO = dO.contiguous()
+        if dO.dtype != u.dtype:
+            dO = dO.to(u.dtype)
+        dO = _aligned(dO)
+        if plan.info.n_kv > 0:
+            _select_dx_mode(int(plan.info.n_kv))
+        du = torch.empty_like(u)
+        dX = torch.empty_like(X)
+        dW_V = torch.empty_like(W_V)
+        L = _lib.lib()
+        ws = _workspace(L.vafa_absorb_bwd_workspace(plan.info, D_KV, D_H), u.device)
+        _lib.check(L.vafa_absorb_bwd(
+            u.data_ptr(), X.data_ptr(), W_V.data_ptr(), O.data_ptr(), dO.data_ptr(),
+            LSE.data_ptr(), du.data_ptr(), dX.data_ptr(), dW_V.data_ptr(),
+            plan.items.data_ptr(), plan.info, D_KV, D_H, _lib.dtype_code(u.dtype),
+            float(ctx.scale), ws.data_ptr() if ws.numel() else None, ws.numel(),
+            _lib.stream_ptr(u.device)))
+        return du, dX, dW_V, None, None, None, None, None, None
+
+
+def target_attn_inner(
+    u: torch.Tensor,
+    X: torch.Tensor,
+    W_V: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    scale: Optional[float] = None,
+    q_chunk_indices: Optional[torch.Tensor] = None,
+    k_chunk_indices: Optional[torch.Tensor] = None,
+    validate: bool = True,
+) -> torch.Tensor:
+    """Inner entry on projected ``u [T_q,H,D_KV]`` (ta/interface.py:324-354)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(W_V.shape[2])
+    return _TargetAttnFunction.apply(
+        u, X, W_V, cu_seqlens_q, cu_seqlens_k, float(scale),
+        q_chunk_indices, k_chunk_indices, validate)
+
+
+def _project_u(q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
+    """u[t,h,:] = (q_raw[t] W_Q[:,h,:]) W_K[:,h,:]^T (ta/interface.py:434-435).
+
+    One 2-D GEMM for all heads of W_Q, then one 2-D GEMM per head for W_K
+    (no batched products; same per-element math as the reference einsum).
+    """
+    T_q, d_q = q_raw.shape
+    _, H, D_H = W_Q.shape
+    q_proj = (q_raw @ W_Q.reshape(d_q, H * D_H)).view(T_q, H, D_H)
+    return torch.stack([q_proj[:, h, :] @ W_K[:, h, :].t() for h in range(H)], dim=1)
+
+
+def packed_target_attn(
+    q_raw: torch.Tensor,
+    X: torch.Tensor,
+    W_Q: torch.Tensor,
+    W_K: torch.Tensor,
+    W_V: torch.Tensor,
+    *,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    cu_seqlens_k: Optional[torch.Tensor] = None,
+    q_seqinfo: Optional[torch.Tensor] = None,
+    k_seqinfo: Optional[torch.Tensor] = None,
+    q_chunk_indices: Optional[torch.Tensor] = None,
+    k_chunk_indices: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    bf16: bool = False,
+    validate: bool = True,
+) -> torch.Tensor:
+    """Full ragged target attention with matrix absorption (ta/interface.py:357-445).
+
+    q_raw ``[T_q,d_q]`` or ``[1,T_q,d_q]``; X ``[T_k,d_kv]`` or ``[1,T_k,d_kv]``;
+    W_Q ``[d_q,H,D_H]``, W_K/W_V ``[d_kv,H,D_H]``.  Returns O ``[T_q,H,D_H]``
+    in the compute dtype (bf16 when ``bf16=True``, else the input dtype).
+    """
+    if q_raw.dim() == 3:
+        assert q_raw.shape[0] == 1, "batch must be 1 for packed varlen"
+        q_raw = q_raw.squeeze(0)
+    if X.dim() == 3:
+        assert X.shape[0] == 1
+        X = X.squeeze(0)
+
+    T_q, d_q = q_raw.shape
+    T_k, d_kv = X.shape
+    d_q_wq, H, D_H = W_Q.shape
+    d_kv_wk, H_wk, D_H_wk = W_K.shape
+    d_kv_wv, H_wv, D_H_wv = W_V.shape
+    assert d_q_wq == d_q, f"W_Q[0]={d_q_wq} != d_q={d_q}"
+    assert d_kv_wk == d_kv and d_kv_wv == d_kv, "W_K/W_V d_kv mismatch"
+    assert H == H_wk == H_wv, "H mismatch across W_Q/W_K/W_V"
+    assert D_H == D_H_wk == D_H_wv, "D_H mismatch across W_Q/W_K/W_V"
+
+    if cu_seqlens_q is None:
+        assert q_seqinfo is not None
+        cu_seqlens_q = _seqinfo_to_cu(q_seqinfo)
+    if cu_seqlens_k is None:
+        assert k_seqinfo is not None
+        cu_seqlens_k = _seqinfo_to_cu(k_seqinfo)
+
+    if bf16:
+        q_raw, X, W_Q, W_K, W_V = (t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+                                   for t in (q_raw, X, W_Q, W_K, W_V))
+
+    u = _project_u(q_raw, W_Q, W_K)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D_H)
+    return target_attn_inner(
+        u, X, W_V, cu_seqlens_q, cu_seqlens_k, scale,
+        q_chunk_indices=q_chunk_indices, k_chunk_indices=k_chunk_indices, validate=validate)
+
+
+def _seqinfo_to_cu(seqinfo: torch.Tensor) -> torch.Tensor:
+    """[n_seg] lengths -> [n_seg+1] int32 (ta/interface.py:448-454: asserts only)."""
+    assert seqinfo.dim() == 1 and seqinfo.numel() >= 1
+    s = _lib.as_host_i64(seqinfo)
+    cu = np.zeros(s.size + 1, dtype=np.int64)
+    cu[1:] = np.cumsum(s)
+    return torch.from_numpy(cu.astype(np.int32)).to(seqinfo.device)

@@ -1,0 +1,293 @@
+// extern "C" entry points: argument checks, workspace carving and kernel
+// dispatch.  Compiled by hipcc (host code only; kernels live in *.hip).
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+#include "../../include/vafa.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace vafa {
+int fail(int code, const char *fmt, ...);
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Sequential carve-out of a caller-provided workspace.
+struct Carver {
+  char *base;
+  int64_t used = 0;
+  explicit Carver(void *b) : base(static_cast<char *>(b)) {}
+  template <typename P>
+  P *take(int64_t bytes) {
+    P *p = base ? reinterpret_cast<P *>(base + used) : nullptr;
+    used += align_up(bytes);
+    return p;
+  }
+};
+
+int check_info(const vafa_plan_info *info, int64_t kind) {
+  if (info == nullptr || info->magic != VAFA_PLAN_MAGIC || info->kind != kind)
+    return fail(VAFA_ERR_VALUE, "plan does not belong to this operator");
+  return VAFA_OK;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(VAFA_ERR_RUNTIME, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  return VAFA_OK;
+}
+
+bool supported_d(int64_t D) {
+  return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
+}
+
+// ---- varlen ---------------------------------------------------------------
+struct VarlenWs {
+  float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr;
+  int64_t bytes = 0;
+};
+
+VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd) {
+  Carver c(ws);
+  VarlenWs w;
+  const int64_t rows = info->n_part_rows * info->H;
+  if (bwd) w.delta = c.take<float>(info->T_q * info->H * 4);
+  w.part_o = c.take<float>(rows * D * 4);
+  if (!bwd) w.part_lse = c.take<float>(rows * 4);
+  w.bytes = c.used;
+  return w;
+}
+
+template <typename T>
+void varlen_fwd_dispatch(const VarlenArgs &a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    switch (a.D) {
+      case 32: launch_mfma_varlen_fwd<T, 32>(a, st); return;
+      case 64: launch_mfma_varlen_fwd<T, 64>(a, st); return;
+      case 128: launch_mfma_varlen_fwd<T, 128>(a, st); return;
+      case 256: launch_mfma_varlen_fwd<T, 256>(a, st); return;
+      default: break;
+    }
+  }
+  launch_simt_varlen_fwd<T>(a, st);
+}
+
+template <typename T>
+void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
+  varlen_fwd_dispatch<T>(a, st);
+  launch_lse_combine<T>(a.part_o, a.part_lse, a.o, a.lse, a.comb_items, a.n_comb, a.H, a.D, st);
+}
+
+template <typename T>
+void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
+  launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
+  launch_simt_varlen_dq<T>(a, st);
+  launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, st);
+  launch_simt_varlen_dkv<T>(a, st);
+}
+
+// ---- absorb ---------------------------------------------------------------
+struct AbsorbWs {
+  float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *dax = nullptr, *ax = nullptr,
+        *dwv_part = nullptr;
+  int64_t n_tchunks = 0, tchunk = 0;
+  int64_t bytes = 0;
+};
+
+constexpr int64_t kDwvChunks = 64;
+
+AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t DH, bool bwd) {
+  Carver c(ws);
+  AbsorbWs w;
+  const int64_t H = info->H, Tq = info->T_q;
+  if (!bwd) {
+    w.part_o = c.take<float>(info->n_part_rows * H * DH * 4);
+    w.part_lse = c.take<float>(info->n_part_rows * H * 4);
+  } else {
+    w.delta = c.take<float>(Tq * H * 4);
+    w.dax = c.take<float>(Tq * H * F * 4);
+    w.ax = c.take<float>(Tq * H * F * 4);
+    w.tchunk = Tq > 0 ? (Tq + kDwvChunks - 1) / kDwvChunks : 0;
+    w.n_tchunks = Tq > 0 ? (Tq + w.tchunk - 1) / w.tchunk : 0;
+    w.dwv_part = c.take<float>((w.n_tchunks > 0 ? w.n_tchunks : 1) * F * H * DH * 4);
+  }
+  w.bytes = c.used;
+  return w;
+}
+
+template <typename T>
+void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (mfma_absorb_supported<T>(a.H, a.F, a.DH)) {
+      launch_mfma_absorb_fwd<T>(a, st);
+    } else {
+      launch_simt_absorb_fwd<T>(a, st);
+    }
+  } else {
+    launch_simt_absorb_fwd<T>(a, st);
+  }
+  launch_lse_combine<T>(a.part_o, a.part_lse, a.O, a.lse, a.comb_items, a.n_comb, a.H, a.DH, st);
+}
+
+template <typename T>
+void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
+  launch_row_dot<T>(a.O_in, a.dO, a.delta, a.T_q * a.H, a.DH, st);
+  launch_absorb_dax<T>(a, st);
+  launch_simt_absorb_du<T>(a, st);
+  launch_simt_absorb_dx<T>(a, st);
+  launch_absorb_dwv<T>(a, st);
+}
+
+template <template <typename> class F, typename A>
+int by_dtype(int32_t dtype, const A &a, hipStream_t st) {
+  switch (dtype) {
+    case VAFA_F32: F<float>::run(a, st); return VAFA_OK;
+    case VAFA_F16: F<f16>::run(a, st); return VAFA_OK;
+    case VAFA_BF16: F<bf16>::run(a, st); return VAFA_OK;
+    default: return fail(VAFA_ERR_ASSERT, "unsupported dtype code %d", (int)dtype);
+  }
+}
+template <typename T> struct VFwd { static void run(const VarlenArgs &a, hipStream_t s) { varlen_fwd_all<T>(a, s); } };
+template <typename T> struct VBwd { static void run(const VarlenArgs &a, hipStream_t s) { varlen_bwd_all<T>(a, s); } };
+template <typename T> struct AFwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_fwd_all<T>(a, s); } };
+template <typename T> struct ABwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_bwd_all<T>(a, s); } };
+
+}  // namespace
+}  // namespace vafa
+
+using namespace vafa;
+
+extern "C" {
+
+const char *vafa_version(void) { return "vafa 0.1.0 gfx950"; }
+
+int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D) {
+  if (check_info(info, 1)) return -1;
+  return carve_varlen(nullptr, info, D, false).bytes;
+}
+
+int64_t vafa_varlen_bwd_workspace(const vafa_plan_info *info, int64_t D) {
+  if (check_info(info, 1)) return -1;
+  return carve_varlen(nullptr, info, D, true).bytes;
+}
+
+int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream) {
+  if (int rc = check_info(info, 1)) return rc;
+  if (!supported_d(D))
+    return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
+  VarlenWs w = carve_varlen(workspace, info, D, false);
+  if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
+    return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  VarlenArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
+  a.part_o = w.part_o; a.part_lse = w.part_lse;
+  a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
+  a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
+  if (int rc = by_dtype<VFwd>(dtype, a, (hipStream_t)stream)) return rc;
+  return check_launch("vafa_varlen_fwd");
+}
+
+int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream) {
+  if (int rc = check_info(info, 1)) return rc;
+  if (!supported_d(D))
+    return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
+  VarlenWs w = carve_varlen(workspace, info, D, true);
+  if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
+    return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  VarlenArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o_in = o; a.dout = dout; a.lse_in = lse;
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  a.delta = w.delta; a.part_o = w.part_o;
+  a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
+  a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
+  if (int rc = by_dtype<VBwd>(dtype, a, (hipStream_t)stream)) return rc;
+  return check_launch("vafa_varlen_bwd");
+}
+
+int64_t vafa_absorb_fwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H) {
+  if (check_info(info, 2)) return -1;
+  return carve_absorb(nullptr, info, D_KV, D_H, false).bytes;
+}
+
+int64_t vafa_absorb_bwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H) {
+  if (check_info(info, 2)) return -1;
+  return carve_absorb(nullptr, info, D_KV, D_H, true).bytes;
+}
+
+static int check_absorb_dims(int64_t F, int64_t DH) {
+  if (!(DH == 16 || DH == 32 || DH == 64 || DH == 128 || DH == 256))
+    return fail(VAFA_ERR_ASSERT, "D_H %lld not supported", (long long)DH);
+  if (F < 1 || F > 512)
+    return fail(VAFA_ERR_ASSERT, "D_KV=%lld pads beyond 512, which is too large", (long long)F);
+  return VAFA_OK;
+}
+
+int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, float *lse,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D_KV,
+                    int64_t D_H, int32_t dtype, float scale, void *workspace,
+                    int64_t workspace_bytes, void *stream) {
+  if (int rc = check_info(info, 2)) return rc;
+  if (int rc = check_absorb_dims(D_KV, D_H)) return rc;
+  AbsorbWs w = carve_absorb(workspace, info, D_KV, D_H, false);
+  if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
+    return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  AbsorbArgs a{};
+  a.u = u; a.X = X; a.wv = W_V; a.O = O; a.lse = lse;
+  a.part_o = w.part_o; a.part_lse = w.part_lse;
+  a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
+  a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
+  a.T_q = info->T_q; a.T_k = info->T_k;
+  a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
+  if (int rc = by_dtype<AFwd>(dtype, a, (hipStream_t)stream)) return rc;
+  return check_launch("vafa_absorb_fwd");
+}
+
+int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O,
+                    const void *dO, const float *lse, void *du, void *dX, void *dW_V,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D_KV,
+                    int64_t D_H, int32_t dtype, float scale, void *workspace,
+                    int64_t workspace_bytes, void *stream) {
+  if (int rc = check_info(info, 2)) return rc;
+  if (int rc = check_absorb_dims(D_KV, D_H)) return rc;
+  AbsorbWs w = carve_absorb(workspace, info, D_KV, D_H, true);
+  if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
+    return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  AbsorbArgs a{};
+  a.u = u; a.X = X; a.wv = W_V; a.O_in = O; a.dO = dO; a.lse_in = lse;
+  a.du = du; a.dX = dX; a.dwv = dW_V;
+  a.delta = w.delta; a.dax = w.dax; a.ax = w.ax; a.dwv_part = w.dwv_part;
+  a.n_tchunks = w.n_tchunks; a.tchunk = w.tchunk;
+  a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
+  a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
+  a.T_q = info->T_q; a.T_k = info->T_k;
+  a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
+  if (int rc = by_dtype<ABwd>(dtype, a, (hipStream_t)stream)) return rc;
+  return check_launch("vafa_absorb_bwd");
+}
+
+}  // extern "C"

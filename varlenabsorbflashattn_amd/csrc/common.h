@@ -1,0 +1,74 @@
+// Device-side helpers shared by every kernel (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "plan_params.h"
+
+namespace vafa {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+// ---- scalar conversions ---------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float to_f(T x) {
+  return static_cast<float>(x);
+}
+template <typename T>
+__device__ __forceinline__ T from_f(float x) {
+  return static_cast<T>(x);
+}
+// Round an fp32 value to T and back (models feeding T-typed matrix inputs).
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  return static_cast<float>(static_cast<T>(x));
+}
+
+// ---- wave reductions (64 lanes) --------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// A 32-byte plan item (see plan.cpp for the per-section field meaning).
+struct alignas(16) PlanItem {
+  int32_t v[8];
+};
+
+__device__ __forceinline__ PlanItem load_item(const int32_t *plan, int64_t idx) {
+  const u32x4 *p = reinterpret_cast<const u32x4 *>(plan + idx * 8);
+  u32x4 a = p[0], b = p[1];
+  PlanItem it;
+  it.v[0] = (int32_t)a[0];
+  it.v[1] = (int32_t)a[1];
+  it.v[2] = (int32_t)a[2];
+  it.v[3] = (int32_t)a[3];
+  it.v[4] = (int32_t)b[0];
+  it.v[5] = (int32_t)b[1];
+  it.v[6] = (int32_t)b[2];
+  it.v[7] = (int32_t)b[3];
+  return it;
+}
+
+}  // namespace vafa

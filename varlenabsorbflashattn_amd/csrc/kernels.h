@@ -1,0 +1,78 @@
+// Launch arguments and launcher declarations shared by the C ABI and the
+// kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vafa {
+
+struct VarlenArgs {
+  const void *q, *k, *v, *o_in, *dout;
+  void *o, *dq, *dk, *dv;
+  float *lse;            // forward output [T_q, H]
+  const float *lse_in;   // backward input [T_q, H]
+  float *delta;          // [T_q, H] workspace (backward)
+  float *part_o;         // split partial rows: O (fwd) or dQ (bwd), [rows, H, D]
+  float *part_lse;       // split partial LSE [rows, H] (fwd)
+  const int32_t *items, *comb_items, *kv_items;
+  int64_t n_items, n_comb, n_kv;
+  int64_t T_q;
+  int H, D;
+  float scale;
+};
+
+struct AbsorbArgs {
+  const void *u, *X, *wv, *O_in, *dO;
+  void *O, *du, *dX, *dwv;
+  float *lse;
+  const float *lse_in;
+  float *delta;
+  float *part_o, *part_lse;   // split partial rows [rows, H, D_H] / [rows, H]
+  float *dax, *ax;            // [T_q, H, F] fp32 (backward)
+  float *dwv_part;            // [n_tchunks, F, H, D_H] fp32 (backward)
+  const int32_t *items, *comb_items, *kv_items, *qseg_items;
+  int64_t n_items, n_comb, n_kv, n_qseg;
+  int64_t T_q, T_k;
+  int64_t n_tchunks, tchunk;
+  int H, F, DH;
+  float scale;
+};
+
+// simt.hip
+template <typename T> void launch_simt_varlen_fwd(const VarlenArgs &, hipStream_t);
+template <typename T> void launch_simt_varlen_dq(const VarlenArgs &, hipStream_t);
+template <typename T> void launch_simt_varlen_dkv(const VarlenArgs &, hipStream_t);
+template <typename T> void launch_simt_absorb_fwd(const AbsorbArgs &, hipStream_t);
+template <typename T> void launch_simt_absorb_du(const AbsorbArgs &, hipStream_t);
+template <typename T> void launch_simt_absorb_dx(const AbsorbArgs &, hipStream_t);
+
+// reduce.hip
+// delta[t,h] = sum_d O[t,h,d] * dO[t,h,d] (fa/kernels.py:186-216)
+template <typename T>
+void launch_row_dot(const void *o, const void *dout, float *delta, int64_t rows, int D,
+                    hipStream_t);
+// LSE-weighted merge of split partials into out / lse (fa/kernels.py:652-734)
+template <typename T>
+void launch_lse_combine(const float *part_o, const float *part_lse, void *out, float *lse,
+                        const int32_t *comb_items, int64_t n_comb, int H, int D, hipStream_t);
+// Plain ordered sum of split partials (dQ): out = sum_s part[s]
+template <typename T>
+void launch_sum_combine(const float *part, void *out, const int32_t *comb_items, int64_t n_comb,
+                        int H, int D, hipStream_t);
+// dW_V = sum_t aX[t]^T dO[t] per head, two-level deterministic reduction.
+template <typename T>
+void launch_absorb_dwv(const AbsorbArgs &, hipStream_t);
+// dAX = dO W_V^T, fp32 [T_q, H, F]
+template <typename T>
+void launch_absorb_dax(const AbsorbArgs &, hipStream_t);
+
+// varlen_mfma.hip (bf16 / f16, D in {32, 64, 128, 256})
+template <typename T, int D> void launch_mfma_varlen_fwd(const VarlenArgs &, hipStream_t);
+template <typename T, int D> void launch_mfma_varlen_dq(const VarlenArgs &, hipStream_t);
+template <typename T, int D> void launch_mfma_varlen_dkv(const VarlenArgs &, hipStream_t);
+
+// absorb_mfma.hip (bf16 / f16)
+template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
+template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
+
+}  // namespace vafa

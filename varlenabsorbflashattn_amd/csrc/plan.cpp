@@ -1,0 +1,327 @@
+// Host-side metadata and work planner for the varlen and absorb operators.
+//
+// Pure C++17, no device calls: everything here runs (and is tested) on a CPU.
+// It replaces the reference's Python metadata layer:
+//   fa/interface.py:74-118          seqinfo -> cu_seqlens, validation
+//   fa/chunk_indices.py:25-65       (seg, block) chunk tables
+//   fa/chunk_indices.py:144-287     short / split / combine dispatch tables
+//   ta/interface.py:92-138          validation, prepare_target_attn_indices
+//   ta/chunk_indices.py:19-67       Q-major and K-major chunk tables
+//
+// Instead of (seg, block) pairs that every GPU program re-resolves through
+// cu_seqlens, a plan holds 32-byte items with absolute token offsets, sorted
+// longest-first (LPT) so that the long-tail tiles start first on a grid of
+// many more workgroups than CUs.  Long key ranges are split; split items write
+// compact partial rows (only the valid query rows) that a combine pass merges
+// in a fixed order, so results are deterministic.
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/vafa.h"
+#include "plan_params.h"
+
+namespace vafa {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+namespace {
+
+struct Item {
+  int32_t v[VAFA_ITEM_INTS];
+  int64_t cost;
+};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+
+// Number of key chunks for one query tile with `rows` valid rows against a
+// segment of `lk` keys, and the chunk length (a multiple of `align`).
+void key_split(int64_t rows, int64_t lk, const SplitPolicy &p, int64_t *ns_out,
+               int64_t *chunk_out) {
+  int64_t ns = 1;
+  if (lk > 0) {
+    if (rows <= p.decode_rows && lk >= p.decode_min_keys) {
+      ns = std::min<int64_t>(std::max<int64_t>(cdiv(lk, p.decode_chunk), p.decode_min_split),
+                             p.decode_max_split);
+    } else if (lk > p.long_threshold) {
+      ns = cdiv(lk, p.long_chunk);
+    }
+  }
+  int64_t chunk = lk > 0 ? round_up(cdiv(lk, ns), p.align) : 0;
+  if (chunk > 0) ns = cdiv(lk, chunk);
+  *ns_out = ns;
+  *chunk_out = chunk;
+}
+
+void sort_lpt(std::vector<Item> &items) {
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item &a, const Item &b) { return a.cost > b.cost; });
+}
+
+int emit(const std::vector<Item> &sec0, const std::vector<Item> &sec1,
+         const std::vector<Item> &sec2, const std::vector<Item> &sec3, int32_t *plan,
+         int64_t cap, vafa_plan_info *info) {
+  info->off_fwd = 0;
+  info->n_fwd = (int64_t)sec0.size();
+  info->off_comb = info->off_fwd + info->n_fwd * VAFA_ITEM_INTS;
+  info->n_comb = (int64_t)sec1.size();
+  info->off_kv = info->off_comb + info->n_comb * VAFA_ITEM_INTS;
+  info->n_kv = (int64_t)sec2.size();
+  info->off_qt = info->off_kv + info->n_kv * VAFA_ITEM_INTS;
+  info->n_qt = (int64_t)sec3.size();
+  info->plan_ints = info->off_qt + info->n_qt * VAFA_ITEM_INTS;
+  if (plan == nullptr) return VAFA_OK;
+  if (cap < info->plan_ints)
+    return fail(VAFA_ERR_CAPACITY, "plan buffer holds %lld int32, %lld needed",
+                (long long)cap, (long long)info->plan_ints);
+  int32_t *p = plan;
+  for (const auto *sec : {&sec0, &sec1, &sec2, &sec3})
+    for (const Item &it : *sec) {
+      std::memcpy(p, it.v, sizeof(it.v));
+      p += VAFA_ITEM_INTS;
+    }
+  return VAFA_OK;
+}
+
+int check_pair(const int64_t *cu_q, const int64_t *cu_k, int64_t n1) {
+  if (n1 < 2) return fail(VAFA_ERR_VALUE, "cu_seqlens must have at least 2 elements");
+  for (int64_t i = 0; i + 1 < n1; ++i) {
+    if (cu_q[i + 1] < cu_q[i] || cu_k[i + 1] < cu_k[i])
+      return fail(VAFA_ERR_VALUE, "cu_seqlens must be non-decreasing");
+  }
+  if (cu_q[0] != 0 || cu_k[0] != 0) return fail(VAFA_ERR_VALUE, "cu_seqlens[0] must be 0");
+  if (cu_q[n1 - 1] > INT32_MAX || cu_k[n1 - 1] > INT32_MAX)
+    return fail(VAFA_ERR_VALUE, "total tokens exceed int32 range");
+  return VAFA_OK;
+}
+
+}  // namespace
+}  // namespace vafa
+
+using namespace vafa;
+
+extern "C" {
+
+const char *vafa_last_error(void) { return g_last_error.c_str(); }
+
+int vafa_seqinfo_to_cu(const int64_t *seqinfo, int64_t n, int32_t *cu_out) {
+  if (n <= 0) return fail(VAFA_ERR_VALUE, "seqinfo is empty (n_seg=0)");
+  for (int64_t i = 0; i < n; ++i)
+    if (seqinfo[i] < 0) return fail(VAFA_ERR_VALUE, "seqinfo contains negative values");
+  int64_t acc = 0;
+  cu_out[0] = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    acc += seqinfo[i];
+    if (acc > INT32_MAX)
+      return fail(VAFA_ERR_VALUE, "total tokens %lld exceeds int32 range", (long long)acc);
+    cu_out[i + 1] = (int32_t)acc;
+  }
+  return VAFA_OK;
+}
+
+int vafa_validate_cu(const int64_t *cu, int64_t n1, int64_t T, const char *name) {
+  if (n1 < 2)
+    return fail(VAFA_ERR_VALUE, "%s: must have at least 2 elements (n_seg+1 with n_seg>=1)",
+                name);
+  if (cu[0] != 0) return fail(VAFA_ERR_VALUE, "%s[0] must be 0, got %lld", name, (long long)cu[0]);
+  if (cu[n1 - 1] != T)
+    return fail(VAFA_ERR_VALUE, "%s[-1] must equal total tokens %lld, got %lld", name,
+                (long long)T, (long long)cu[n1 - 1]);
+  for (int64_t i = 0; i + 1 < n1; ++i)
+    if (cu[i + 1] < cu[i])
+      return fail(VAFA_ERR_VALUE, "%s must be non-decreasing (found negative segment length)",
+                  name);
+  return VAFA_OK;
+}
+
+int vafa_check_active_have_keys(const int64_t *cu_q, const int64_t *cu_k, int64_t n1) {
+  for (int64_t i = 0; i + 1 < n1; ++i)
+    if (cu_q[i + 1] - cu_q[i] > 0 && cu_k[i + 1] - cu_k[i] <= 0)
+      return fail(VAFA_ERR_VALUE, "segments with q_len > 0 must have k_len > 0");
+  return VAFA_OK;
+}
+
+int vafa_chunk_indices(const int64_t *cu, int64_t n1, int32_t BT, int32_t *out, int64_t cap,
+                       int64_t *n_rows) {
+  if (BT < 1) return fail(VAFA_ERR_ASSERT, "BT must be >= 1");
+  if (n1 < 2) return fail(VAFA_ERR_ASSERT, "cu_seqlens must be 1-D with len >= 2");
+  int64_t total = 0;
+  for (int64_t i = 0; i + 1 < n1; ++i) {
+    int64_t L = cu[i + 1] - cu[i];
+    if (L > 0) total += cdiv(L, BT);
+  }
+  *n_rows = total;
+  if (total > cap) return fail(VAFA_ERR_CAPACITY, "chunk table needs %lld rows", (long long)total);
+  int64_t r = 0;
+  for (int64_t i = 0; i + 1 < n1; ++i) {
+    int64_t L = cu[i + 1] - cu[i];
+    int64_t nb = L > 0 ? cdiv(L, BT) : 0;
+    for (int64_t b = 0; b < nb; ++b, ++r) {
+      out[2 * r] = (int32_t)i;
+      out[2 * r + 1] = (int32_t)b;
+    }
+  }
+  return VAFA_OK;
+}
+
+// Varlen plan.
+//   fwd section   : one item per (segment, query tile, key chunk):
+//                   {q0, q1, k0, k1, pbase, seg, split, nsplit}; pbase = -1
+//                   writes O/LSE directly, otherwise partial rows
+//                   pbase + r (r < q1-q0) hold this chunk's normalized O and LSE.
+//   comb section  : one item per split query tile:
+//                   {q0, q1, pbase, nsplit, seg, 0, 0, 0}; split s of the tile
+//                   owns partial rows pbase + s*(q1-q0) + r.
+//   kv section    : one item per (segment, key tile) for dK/dV:
+//                   {k0, k1, q0, q1, seg, 0, 0, 0} with [q0,q1) the segment's
+//                   whole query range.
+// The dQ pass reuses the fwd and comb sections with its own partial buffer.
+int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H, int64_t D,
+                     int32_t *plan, int64_t plan_cap, vafa_plan_info *info) {
+  int rc = check_pair(cu_q, cu_k, n1);
+  if (rc) return rc;
+  const SplitPolicy &pol = kVarlenPolicy;
+  const int64_t BM = kVarlenQTile, BK = kVarlenKTile;
+  std::memset(info, 0, sizeof(*info));
+  info->magic = VAFA_PLAN_MAGIC;
+  info->kind = 1;
+  info->n_seg = n1 - 1;
+  info->T_q = cu_q[n1 - 1];
+  info->T_k = cu_k[n1 - 1];
+  info->H = H;
+  info->q_tile = BM;
+  info->k_tile = BK;
+  (void)D;
+  std::vector<Item> fwd, comb, kv;
+  int64_t prow = 0;
+  int64_t max_split = 1;
+  for (int64_t s = 0; s + 1 < n1; ++s) {
+    const int64_t q0 = cu_q[s], q1 = cu_q[s + 1], k0 = cu_k[s], k1 = cu_k[s + 1];
+    const int64_t lq = q1 - q0, lk = k1 - k0;
+    for (int64_t t = q0; t < q1; t += BM) {
+      const int64_t te = std::min(t + BM, q1), rows = te - t;
+      int64_t ns, chunk;
+      key_split(rows, lk, pol, &ns, &chunk);
+      max_split = std::max(max_split, ns);
+      if (ns <= 1) {
+        Item it{{(int32_t)t, (int32_t)te, (int32_t)k0, (int32_t)k1, -1, (int32_t)s, 0, 1},
+                lk + pol.item_overhead};
+        fwd.push_back(it);
+        continue;
+      }
+      Item c{{(int32_t)t, (int32_t)te, (int32_t)prow, (int32_t)ns, (int32_t)s, 0, 0, 0}, 0};
+      comb.push_back(c);
+      for (int64_t j = 0; j < ns; ++j) {
+        const int64_t a = k0 + j * chunk, b = std::min(k1, a + chunk);
+        Item it{{(int32_t)t, (int32_t)te, (int32_t)a, (int32_t)b, (int32_t)(prow + j * rows),
+                 (int32_t)s, (int32_t)j, (int32_t)ns},
+                (b - a) + pol.item_overhead};
+        fwd.push_back(it);
+      }
+      prow += ns * rows;
+    }
+    for (int64_t k = k0; k < k1; k += BK) {
+      const int64_t ke = std::min(k + BK, k1);
+      Item it{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s, 0, 0, 0},
+              lq + pol.item_overhead};
+      kv.push_back(it);
+    }
+  }
+  sort_lpt(fwd);
+  sort_lpt(kv);
+  info->n_part_rows = prow;
+  info->max_split = max_split;
+  return emit(fwd, comb, kv, {}, plan, plan_cap, info);
+}
+
+// Absorb plan.  Query rows are (token, head) pairs; one item covers whole
+// tokens [t0, t1) with (t1 - t0) * H <= kAbsorbRows.
+//   fwd section : {t0, t1, k0, k1, pbase, seg, split, nsplit}; split items
+//                 write projected partial rows pbase + r (r < t1-t0), each
+//                 holding H x D_H fp32 outputs and H log2-domain LSEs.
+//   comb section: {t0, t1, pbase, nsplit, seg, 0, 0, 0}.
+//   kv section  : {k0, k1, t0, t1, seg, 0, 0, 0} key tiles for dX with the
+//                 segment's whole token range [t0, t1).
+//   qt section  : {t0, t1, k0, k1, -1, seg, 0, 1} unsplit token tiles with the
+//                 segment's whole key range (backward dU pass).
+int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H,
+                     int64_t D_KV, int64_t D_H, int32_t *plan, int64_t plan_cap,
+                     vafa_plan_info *info) {
+  int rc = check_pair(cu_q, cu_k, n1);
+  if (rc) return rc;
+  if (H < 1) return fail(VAFA_ERR_ASSERT, "H must be >= 1");
+  (void)D_KV;
+  (void)D_H;
+  const SplitPolicy &pol = kAbsorbPolicy;
+  const int64_t TT = std::max<int64_t>(1, kAbsorbRows / H);
+  const int64_t BK = kAbsorbKTile;
+  std::memset(info, 0, sizeof(*info));
+  info->magic = VAFA_PLAN_MAGIC;
+  info->kind = 2;
+  info->n_seg = n1 - 1;
+  info->T_q = cu_q[n1 - 1];
+  info->T_k = cu_k[n1 - 1];
+  info->H = H;
+  info->q_tile = TT;
+  info->k_tile = BK;
+  std::vector<Item> fwd, comb, kv, qt;
+  int64_t prow = 0, max_split = 1;
+  for (int64_t s = 0; s + 1 < n1; ++s) {
+    const int64_t q0 = cu_q[s], q1 = cu_q[s + 1], k0 = cu_k[s], k1 = cu_k[s + 1];
+    const int64_t lq = q1 - q0, lk = k1 - k0;
+    for (int64_t t = q0; t < q1; t += TT) {
+      const int64_t te = std::min(t + TT, q1), ntok = te - t;
+      int64_t ns, chunk;
+      key_split(ntok * H, lk, pol, &ns, &chunk);
+      max_split = std::max(max_split, ns);
+      const int64_t row_cost = round_up(ntok * H, 32);
+      qt.push_back(Item{{(int32_t)t, (int32_t)te, (int32_t)k0, (int32_t)k1, -1, (int32_t)s, 0, 1},
+                        (lk + pol.item_overhead) * row_cost});
+      if (ns <= 1) {
+        Item it{{(int32_t)t, (int32_t)te, (int32_t)k0, (int32_t)k1, -1, (int32_t)s, 0, 1},
+                (lk + pol.item_overhead) * row_cost};
+        fwd.push_back(it);
+        continue;
+      }
+      Item c{{(int32_t)t, (int32_t)te, (int32_t)prow, (int32_t)ns, (int32_t)s, 0, 0, 0}, 0};
+      comb.push_back(c);
+      for (int64_t j = 0; j < ns; ++j) {
+        const int64_t a = k0 + j * chunk, b = std::min(k1, a + chunk);
+        Item it{{(int32_t)t, (int32_t)te, (int32_t)a, (int32_t)b, (int32_t)(prow + j * ntok),
+                 (int32_t)s, (int32_t)j, (int32_t)ns},
+                ((b - a) + pol.item_overhead) * row_cost};
+        fwd.push_back(it);
+      }
+      prow += ns * ntok;
+    }
+    for (int64_t k = k0; k < k1; k += BK) {
+      const int64_t ke = std::min(k + BK, k1);
+      Item it{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s, 0, 0, 0},
+              (lq * H + pol.item_overhead)};
+      kv.push_back(it);
+    }
+  }
+  sort_lpt(fwd);
+  sort_lpt(kv);
+  sort_lpt(qt);
+  info->n_part_rows = prow;
+  info->max_split = max_split;
+  return emit(fwd, comb, kv, qt, plan, plan_cap, info);
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// Tile sizes and key-split policy shared by the planner and the kernels.
+#pragma once
+#include <cstdint>
+
+namespace vafa {
+
+// Varlen: a forward / dQ workgroup covers kVarlenQTile query rows (4 waves x 32
+// rows); a dK/dV workgroup covers kVarlenKTile keys (4 waves x 32 keys).
+constexpr int kVarlenQTile = 128;
+constexpr int kVarlenKTile = 128;
+// Absorb: a forward workgroup covers up to kAbsorbRows (token, head) rows;
+// a dX workgroup covers kAbsorbKTile keys.
+constexpr int kAbsorbRows = 128;
+constexpr int kAbsorbKTile = 64;
+
+struct SplitPolicy {
+  // Query tiles with at most `decode_rows` rows against >= decode_min_keys
+  // keys are split into clamp(ceil(Lk/decode_chunk), min, max) chunks.
+  int64_t decode_rows, decode_min_keys, decode_chunk, decode_min_split, decode_max_split;
+  // Any other tile is split into ceil(Lk/long_chunk) chunks once
+  // Lk > long_threshold (fa/interface.py:46-57 uses 4096 / 4096).
+  int64_t long_threshold, long_chunk;
+  int64_t align;          // chunk lengths are multiples of this many keys
+  int64_t item_overhead;  // fixed per-item cost (keys-equivalent) for LPT
+};
+
+constexpr SplitPolicy kVarlenPolicy{16, 1024, 2048, 4, 16, 4096, 4096, 64, 64};
+constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 2048, 1024, 64, 32};
+
+}  // namespace vafa

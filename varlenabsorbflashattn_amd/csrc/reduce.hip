@@ -1,0 +1,186 @@
+// Small bandwidth-bound passes shared by both operators: the backward row
+// dot (delta), the split-K merges and the absorb dAX / dW_V reductions.
+// Every reduction runs in a fixed order, so results are bit-reproducible.
+#include "common.h"
+#include "kernels.h"
+
+namespace vafa {
+
+namespace {
+
+// delta[r] = sum_d o[r,d] * dout[r,d] in fp32, one row per thread
+// (fa/kernels.py:186-216, ta/kernels.py:298-325).
+template <typename T>
+__global__ __launch_bounds__(256) void row_dot_kernel(const T *__restrict__ o,
+                                                      const T *__restrict__ dout,
+                                                      float *__restrict__ delta, int64_t rows,
+                                                      int D) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const T *a = o + r * D;
+  const T *b = dout + r * D;
+  float s = 0.f;
+  for (int d = 0; d < D; ++d) s += to_f(a[d]) * to_f(b[d]);
+  delta[r] = s;
+}
+
+// Split-K merge in the log2 domain (fa/kernels.py:639-647):
+//   m = max_s lse_s, w_s = exp2(lse_s - m), O = sum_s w_s O_s / sum_s w_s,
+//   LSE = m + log2(sum_s w_s); every split of a tile is non-empty.
+template <typename T>
+__global__ __launch_bounds__(256) void lse_combine_kernel(
+    const float *__restrict__ part_o, const float *__restrict__ part_lse, T *__restrict__ out,
+    float *__restrict__ lse, const int32_t *__restrict__ items, int H, int D) {
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int q0 = it.v[0], q1 = it.v[1], pbase = it.v[2], ns = it.v[3];
+  const int R = q1 - q0;
+  for (int idx = threadIdx.x; idx < R * D; idx += 256) {
+    const int r = idx / D, d = idx % D;
+    float m = kNegInf;
+    for (int s = 0; s < ns; ++s)
+      m = fmaxf(m, part_lse[(int64_t)(pbase + s * R + r) * H + h]);
+    const float ms = m == kNegInf ? 0.f : m;
+    float l = 0.f, acc = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const int64_t pr = (int64_t)(pbase + s * R + r) * H + h;
+      const float w = fast_exp2(part_lse[pr] - ms);
+      l += w;
+      acc += w * part_o[pr * D + d];
+    }
+    const float ls = l == 0.f ? 1.f : l;
+    out[((int64_t)(q0 + r) * H + h) * D + d] = from_f<T>(acc / ls);
+    if (d == 0) lse[(int64_t)(q0 + r) * H + h] = m == kNegInf ? kNegInf : ms + fast_log2(ls);
+  }
+}
+
+// Ordered sum of split partials (dQ): out = sum_s part[s] (partials carry the
+// softmax scale already).
+template <typename T>
+__global__ __launch_bounds__(256) void sum_combine_kernel(const float *__restrict__ part,
+                                                          T *__restrict__ out,
+                                                          const int32_t *__restrict__ items,
+                                                          int H, int D) {
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int q0 = it.v[0], q1 = it.v[1], pbase = it.v[2], ns = it.v[3];
+  const int R = q1 - q0;
+  for (int idx = threadIdx.x; idx < R * D; idx += 256) {
+    const int r = idx / D, d = idx % D;
+    float acc = 0.f;
+    for (int s = 0; s < ns; ++s) acc += part[((int64_t)(pbase + s * R + r) * H + h) * D + d];
+    out[((int64_t)(q0 + r) * H + h) * D + d] = from_f<T>(acc);
+  }
+}
+
+// dAX[t,h,f] = sum_d dO[t,h,d] W_V[f,h,d]; one block per (t, h) row.
+template <typename T>
+__global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ dO,
+                                                         const T *__restrict__ wv,
+                                                         float *__restrict__ dax, int H, int F,
+                                                         int DH) {
+  const int64_t row = blockIdx.x;
+  const int h = (int)(row % H);
+  __shared__ float sdo[256];
+  for (int d = threadIdx.x; d < DH; d += 256) sdo[d] = to_f(dO[row * DH + d]);
+  __syncthreads();
+  for (int f = threadIdx.x; f < F; f += 256) {
+    const T *w = wv + ((int64_t)f * H + h) * DH;
+    float s = 0.f;
+    for (int d = 0; d < DH; ++d) s += sdo[d] * to_f(w[d]);
+    dax[row * F + f] = s;
+  }
+}
+
+// dW_V partial over one token chunk: part[c, f, h, d] = sum_{t in chunk} aX[t,h,f] dO[t,h,d]
+template <typename T>
+__global__ __launch_bounds__(256) void absorb_dwv_part_kernel(
+    const float *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
+    int64_t T_q, int64_t tchunk, int H, int F, int DH) {
+  const int64_t n_out = (int64_t)F * H * DH;
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n_out) return;
+  const int d = (int)(o % DH);
+  const int h = (int)((o / DH) % H);
+  const int f = (int)(o / ((int64_t)DH * H));
+  const int64_t c = blockIdx.y;
+  const int64_t t0 = c * tchunk, t1 = t0 + tchunk < T_q ? t0 + tchunk : T_q;
+  float s = 0.f;
+  for (int64_t t = t0; t < t1; ++t)
+    s += ax[(t * H + h) * F + f] * to_f(dO[(t * H + h) * DH + d]);
+  part[c * n_out + o] = s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void absorb_dwv_sum_kernel(const float *__restrict__ part,
+                                                             T *__restrict__ dwv, int64_t n_out,
+                                                             int64_t n_chunks) {
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n_out) return;
+  float s = 0.f;
+  for (int64_t c = 0; c < n_chunks; ++c) s += part[c * n_out + o];
+  dwv[o] = from_f<T>(s);
+}
+
+inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+template <typename T>
+void launch_row_dot(const void *o, const void *dout, float *delta, int64_t rows, int D,
+                    hipStream_t st) {
+  if (rows == 0) return;
+  hipLaunchKernelGGL(row_dot_kernel<T>, dim3(blocks_for(rows)), dim3(256), 0, st,
+                     (const T *)o, (const T *)dout, delta, rows, D);
+}
+
+template <typename T>
+void launch_lse_combine(const float *part_o, const float *part_lse, void *out, float *lse,
+                        const int32_t *comb_items, int64_t n_comb, int H, int D, hipStream_t st) {
+  if (n_comb == 0) return;
+  hipLaunchKernelGGL(lse_combine_kernel<T>, dim3((unsigned)(n_comb * H)), dim3(256), 0, st,
+                     part_o, part_lse, (T *)out, lse, comb_items, H, D);
+}
+
+template <typename T>
+void launch_sum_combine(const float *part, void *out, const int32_t *comb_items, int64_t n_comb,
+                        int H, int D, hipStream_t st) {
+  if (n_comb == 0) return;
+  hipLaunchKernelGGL(sum_combine_kernel<T>, dim3((unsigned)(n_comb * H)), dim3(256), 0, st,
+                     part, (T *)out, comb_items, H, D);
+}
+
+template <typename T>
+void launch_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
+  if (a.T_q == 0) return;
+  hipLaunchKernelGGL(absorb_dax_kernel<T>, dim3((unsigned)(a.T_q * a.H)), dim3(256), 0, st,
+                     (const T *)a.dO, (const T *)a.wv, a.dax, a.H, a.F, a.DH);
+}
+
+template <typename T>
+void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
+  const int64_t n_out = (int64_t)a.F * a.H * a.DH;
+  if (a.n_tchunks > 0) {
+    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3(blocks_for(n_out), (unsigned)a.n_tchunks),
+                       dim3(256), 0, st, a.ax, (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H,
+                       a.F, a.DH);
+  }
+  hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st,
+                     a.dwv_part, (T *)a.dwv, n_out, a.n_tchunks);
+}
+
+#define VAFA_INST(T)                                                                        \
+  template void launch_row_dot<T>(const void *, const void *, float *, int64_t, int,        \
+                                  hipStream_t);                                             \
+  template void launch_lse_combine<T>(const float *, const float *, void *, float *,        \
+                                      const int32_t *, int64_t, int, int, hipStream_t);     \
+  template void launch_sum_combine<T>(const float *, void *, const int32_t *, int64_t, int, \
+                                      int, hipStream_t);                                    \
+  template void launch_absorb_dax<T>(const AbsorbArgs &, hipStream_t);                      \
+  template void launch_absorb_dwv<T>(const AbsorbArgs &, hipStream_t);
+VAFA_INST(float)
+VAFA_INST(f16)
+VAFA_INST(bf16)
+#undef VAFA_INST
+
+}  // namespace vafa

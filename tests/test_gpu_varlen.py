@@ -87,7 +87,8 @@ def test_varlen_input_scales(device, dist):
 
 
 def test_single_key_returns_v(device):
-    """Lk = 1: softmax weight 1 -> O == V exactly; dq = dk = 0."""
+    """Lk = 1: softmax weight 1 -> O == V exactly; dq = dk = 0 up to fp32 rounding
+    (delta = O.dO and dP = dO.V are summed in different orders)."""
     H, D = 2, 64
     q = torch.randn(5, H, D, device=device, dtype=torch.bfloat16, requires_grad=True)
     k = torch.randn(1, H, D, device=device, dtype=torch.bfloat16, requires_grad=True)
@@ -96,7 +97,7 @@ def test_single_key_returns_v(device):
                            cu_seqlens_k=torch.tensor([0, 1], device=device))
     assert torch.equal(o, v.expand(5, H, D))
     o.backward(torch.randn_like(o))
-    assert q.grad.abs().max().item() == 0.0 and k.grad.abs().max().item() == 0.0
+    assert q.grad.abs().max().item() < 1e-5 and k.grad.abs().max().item() < 1e-5
 
 
 def test_one_hot_segment_values(device):

@@ -84,18 +84,36 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
   launch_lse_combine<T>(a.part_o, a.part_lse, a.o, a.lse, a.comb_items, a.n_comb, a.H, a.D, st);
 }
 
+// Matrix-core backward for D in {32, 64, 128}; D=16 and D=256 (whose dK/dV
+// accumulators exceed the register file) take the wave-per-row kernels.
+template <typename T>
+bool varlen_bwd_mfma(const VarlenArgs &a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    switch (a.D) {
+      case 32: launch_mfma_varlen_dq<T, 32>(a, st); launch_mfma_varlen_dkv<T, 32>(a, st); return true;
+      case 64: launch_mfma_varlen_dq<T, 64>(a, st); launch_mfma_varlen_dkv<T, 64>(a, st); return true;
+      case 128: launch_mfma_varlen_dq<T, 128>(a, st); launch_mfma_varlen_dkv<T, 128>(a, st); return true;
+      default: break;
+    }
+  }
+  return false;
+}
+
 template <typename T>
 void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
   launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
-  launch_simt_varlen_dq<T>(a, st);
+  if (!varlen_bwd_mfma<T>(a, st)) {
+    launch_simt_varlen_dq<T>(a, st);
+    launch_simt_varlen_dkv<T>(a, st);
+  }
   launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, st);
-  launch_simt_varlen_dkv<T>(a, st);
 }
 
 // ---- absorb ---------------------------------------------------------------
 struct AbsorbWs {
   float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *dax = nullptr, *ax = nullptr,
         *dwv_part = nullptr;
+  void *wvt = nullptr;
   int64_t n_tchunks = 0, tchunk = 0;
   int64_t bytes = 0;
 };
@@ -109,6 +127,7 @@ AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t D
   if (!bwd) {
     w.part_o = c.take<float>(info->n_part_rows * H * DH * 4);
     w.part_lse = c.take<float>(info->n_part_rows * H * 4);
+    w.wvt = c.take<char>(mfma_absorb_wvt_elems((int)H, (int)F, (int)DH) * 2);
   } else {
     w.delta = c.take<float>(Tq * H * 4);
     w.dax = c.take<float>(Tq * H * F * 4);
@@ -253,7 +272,7 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
                 (long long)workspace_bytes, (long long)w.bytes);
   AbsorbArgs a{};
   a.u = u; a.X = X; a.wv = W_V; a.O = O; a.lse = lse;
-  a.part_o = w.part_o; a.part_lse = w.part_lse;
+  a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;

@@ -30,6 +30,7 @@ struct AbsorbArgs {
   float *part_o, *part_lse;   // split partial rows [rows, H, D_H] / [rows, H]
   float *dax, *ax;            // [T_q, H, F] fp32 (backward)
   float *dwv_part;            // [n_tchunks, F, H, D_H] fp32 (backward)
+  void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
   const int32_t *items, *comb_items, *kv_items, *qseg_items;
   int64_t n_items, n_comb, n_kv, n_qseg;
   int64_t T_q, T_k;
@@ -73,6 +74,7 @@ template <typename T, int D> void launch_mfma_varlen_dkv(const VarlenArgs &, hip
 
 // absorb_mfma.hip (bf16 / f16)
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
+int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
 
 }  // namespace vafa

@@ -51,6 +51,22 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// ---- raw buffer loads ----------------------------------------------------
+// A buffer resource covering `bytes` from `base`; loads at offsets >= bytes
+// return zero, which replaces per-lane bounds branches on tile tails.  The
+// base must be wave-uniform and the range below 4 GiB.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// Wave-uniform "any lane" vote.
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 // A 32-byte plan item (see plan.cpp for the per-section field meaning).
 struct alignas(16) PlanItem {
   int32_t v[8];

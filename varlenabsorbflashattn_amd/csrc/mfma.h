@@ -59,6 +59,32 @@ __device__ __forceinline__ u32x4 join(u32x2 a, u32x2 b) {
   return r;
 }
 
+// ---- transposed operand reads from row-major LDS tiles -------------------
+// ds_read_b64_tr_b16: within each 16-lane group, source lane 4e+a supplies
+// 4 consecutive elements (row e, columns 4a..4a+3 of a 4 x 16 block) and
+// output lane i receives column i of that block (rows e = 0..3).
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ u32x2 lds_tr16(const T *p) {
+  typedef v4s16 __attribute__((address_space(3))) * lds_ptr;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p)));
+}
+
+// A operand of a 32x32x16 MFMA whose row index is a column c0 + (l % 32) of
+// a row-major LDS tile (stride elements per row) and whose reduction index
+// runs over tile rows k0 .. k0+15 in the relabelled order of the C layout:
+// B slot (l/32)*8 + t <-> row k0 + (t/4)*8 + (l/32)*4 + t%4.  Two transposed
+// reads cover t = 0..3 and t = 4..7.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 tr_operand(const T *tile, int stride, int k0,
+                                                           int c0, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const T *p = tile + (k0 + 4 * (g >> 1) + (i >> 2)) * stride + c0 + (g & 1) * 16 + 4 * (i & 3);
+  const u32x2 lo = lds_tr16(p);
+  const u32x2 hi = lds_tr16(p + 8 * stride);
+  return as_v8<T>(join(lo, hi));
+}
+
 // 16-bit element e (0..7) of a 16-byte chunk.
 __device__ __forceinline__ uint32_t half_of(const u32x4 &x, int e) {
   return (x[e >> 1] >> ((e & 1) * 16)) & 0xffffu;

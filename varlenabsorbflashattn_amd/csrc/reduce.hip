@@ -8,20 +8,30 @@ namespace vafa {
 
 namespace {
 
-// delta[r] = sum_d o[r,d] * dout[r,d] in fp32, one row per thread
-// (fa/kernels.py:186-216, ta/kernels.py:298-325).
+// delta[r] = sum_d o[r,d] * dout[r,d] in fp32 (fa/kernels.py:186-216,
+// ta/kernels.py:298-325).  Each thread reads one 16-byte chunk of a row; the
+// D/CH threads of a row reduce with lane shuffles, so loads are coalesced.
 template <typename T>
 __global__ __launch_bounds__(256) void row_dot_kernel(const T *__restrict__ o,
                                                       const T *__restrict__ dout,
                                                       float *__restrict__ delta, int64_t rows,
                                                       int D) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const T *a = o + r * D;
-  const T *b = dout + r * D;
+  constexpr int CH = 16 / sizeof(T);  // elements per 16-byte chunk
+  const int tpr = D / CH;             // threads per row (power of two, <= 64)
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = g / tpr;
+  const int part = (int)(g % tpr);
   float s = 0.f;
-  for (int d = 0; d < D; ++d) s += to_f(a[d]) * to_f(b[d]);
-  delta[r] = s;
+  if (r < rows) {
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(o + r * D + part * CH);
+    const u32x4 b = *reinterpret_cast<const u32x4 *>(dout + r * D + part * CH);
+    const T *x = reinterpret_cast<const T *>(&a);
+    const T *y = reinterpret_cast<const T *>(&b);
+#pragma unroll
+    for (int e = 0; e < CH; ++e) s += to_f(x[e]) * to_f(y[e]);
+  }
+  for (int off = tpr >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (r < rows && part == 0) delta[r] = s;
 }
 
 // Split-K merge in the log2 domain (fa/kernels.py:639-647):
@@ -130,7 +140,8 @@ template <typename T>
 void launch_row_dot(const void *o, const void *dout, float *delta, int64_t rows, int D,
                     hipStream_t st) {
   if (rows == 0) return;
-  hipLaunchKernelGGL(row_dot_kernel<T>, dim3(blocks_for(rows)), dim3(256), 0, st,
+  const int64_t threads = rows * (D / (16 / (int)sizeof(T)));
+  hipLaunchKernelGGL(row_dot_kernel<T>, dim3(blocks_for(threads)), dim3(256), 0, st,
                      (const T *)o, (const T *)dout, delta, rows, D);
 }
 

@@ -79,7 +79,7 @@ __device__ __forceinline__ void store_quads(const Quads<D, NT> &s, T *rm, int RS
 // needs rows 16m + lhalf*4 + {0..3} and 16m + 8 + lhalf*4 + {0..3} of column
 // `col` from a transposed LDS tile (row = column index, stride TS).
 template <typename T>
-__device__ __forceinline__ typename Mfma<T>::v8 tr_operand(const T *tr, int TS, int col, int m,
+__device__ __forceinline__ typename Mfma<T>::v8 tr_operand_t(const T *tr, int TS, int col, int m,
                                                            int lhalf) {
   const T *p = tr + col * TS + m * 16 + lhalf * 4;
   const u32x2 lo = *reinterpret_cast<const u32x2 *>(p);
@@ -215,8 +215,8 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
         const int col = dtile * 32 + lrow;
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
-          adv[dtile] = M::mma(tr_operand<T>(dt_, S::TS, col, mm, lhalf), pb[mm], adv[dtile]);
-          adk[dtile] = M::mma(tr_operand<T>(qt, S::TS, col, mm, lhalf), sb[mm], adk[dtile]);
+          adv[dtile] = M::mma(tr_operand_t<T>(dt_, S::TS, col, mm, lhalf), pb[mm], adv[dtile]);
+          adk[dtile] = M::mma(tr_operand_t<T>(qt, S::TS, col, mm, lhalf), sb[mm], adk[dtile]);
         }
       }
     }
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
         const int col = dtile * 32 + lrow;
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          acc[dtile] = M::mma(tr_operand<T>(kt, S::TS, col, mm, lhalf), sb[mm], acc[dtile]);
+          acc[dtile] = M::mma(tr_operand_t<T>(kt, S::TS, col, mm, lhalf), sb[mm], acc[dtile]);
       }
     }
     if (j + 1 < nblk) put((j + 1) & 1);

@@ -3,7 +3,8 @@
 // Forward (replaces fa/kernels.py:64-175 and the split variant 516-628):
 // one workgroup = 4 waves = 128 query rows of one head; each wave owns 32
 // rows.  Key/value tiles of 64 keys are staged once per workgroup in LDS
-// (K row-major, V transposed) with a register prefetch of the next tile, so
+// (both row-major; V^T operands come from transposing LDS reads) with a
+// register prefetch of the next tile, so
 // each tile is read from HBM/L2 once for 128 queries.  Per 64-key tile a wave
 // issues 16 MFMAs for S^T = K Q^T and 16 for O^T += V^T P^T (D=128).  The
 // online softmax runs in the log2 domain, the row max needs one cross-lane
@@ -18,24 +19,20 @@ namespace {
 constexpr int kBM = kVarlenQTile;  // 128 query rows per workgroup
 constexpr int kBN = 64;            // keys per LDS tile
 constexpr int kKPad = 8;           // K row padding (elements)
-constexpr int kVPad = 4;           // V^T row padding (elements)
 
 template <int D>
 struct FwdSmem {
-  static constexpr int kKs = kBN * (D + kKPad);  // elements per K buffer
-  static constexpr int kVt = D * (kBN + kVPad);  // elements per V^T buffer
-  static constexpr int kBuf = kKs + kVt;
+  static constexpr int kKs = kBN * (D + kKPad);  // elements per K (or V) buffer
+  static constexpr int kBuf = 2 * kKs;           // K and V, both row-major
   static constexpr int kBytes = 2 * kBuf * 2;    // double buffered, 2 B/elt
 };
 
 // Global -> register stage of one K/V tile (zero-filled past k_end).
 template <int D>
 struct TileRegs {
-  static constexpr int kKChunks = kBN * D / 8 / 256;           // 16 B chunks per thread
-  static constexpr int kVQuads = (kBN / 4) * (D / 8);          // 4-key x 8-d quads
-  static constexpr int kVPer = (kVQuads + 255) / 256;
-  u32x4 kc[kKChunks > 0 ? kKChunks : 1];
-  u32x4 vq[kVPer][4];
+  static constexpr int kKChunks = kBN * D / 8 / 256;  // 16 B chunks per thread
+  u32x4 kc[kKChunks];
+  u32x4 vc[kKChunks];
 };
 
 template <typename T, int D>
@@ -43,53 +40,113 @@ __device__ __forceinline__ void load_tile(TileRegs<D> &r, const T *__restrict__ 
                                           const T *__restrict__ v, int kbase, int k_end, int H,
                                           int h, int tid) {
   constexpr int CPR = D / 8;  // chunks per row
+  // one buffer resource per tile: rows past k_end read as zero
+  const int64_t row_bytes = (int64_t)H * D * 2;
+  const int64_t nbytes = (int64_t)(k_end - kbase < kBN ? k_end - kbase : kBN) * row_bytes;
+  const rsrc_t rk = make_rsrc(k + (int64_t)kbase * H * D, nbytes);
+  const rsrc_t rv = make_rsrc(v + (int64_t)kbase * H * D, nbytes);
 #pragma unroll
   for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
     const int ci = tid + 256 * i;
     const int key = ci / CPR, dc = ci % CPR;
-    const int gk = kbase + key;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (gk < k_end) val = *reinterpret_cast<const u32x4 *>(k + ((int64_t)gk * H + h) * D + dc * 8);
-    r.kc[i] = val;
+    r.kc[i] = buf_load16(rk, (key * H + h) * D * 2 + dc * 16);
   }
 #pragma unroll
-  for (int i = 0; i < TileRegs<D>::kVPer; ++i) {
-    const int qi = tid + 256 * i;
-    const int kq = qi / CPR, dc = qi % CPR;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int gk = kbase + kq * 4 + e;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (qi < TileRegs<D>::kVQuads && gk < k_end)
-        val = *reinterpret_cast<const u32x4 *>(v + ((int64_t)gk * H + h) * D + dc * 8);
-      r.vq[i][e] = val;
-    }
+  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
+    const int ci = tid + 256 * i;
+    const int key = ci / CPR, dc = ci % CPR;
+    r.vc[i] = buf_load16(rv, (key * H + h) * D * 2 + dc * 16);
   }
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D> &r, T *ks, T *vt, int tid) {
+__device__ __forceinline__ void store_tile(const TileRegs<D> &r, T *ks, T *vs, int tid) {
   constexpr int CPR = D / 8;
-  constexpr int KS = D + kKPad, VS = kBN + kVPad;
+  constexpr int KS = D + kKPad;
 #pragma unroll
   for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
     const int ci = tid + 256 * i;
     const int key = ci / CPR, dc = ci % CPR;
     *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = r.kc[i];
+    *reinterpret_cast<u32x4 *>(vs + key * KS + dc * 8) = r.vc[i];
   }
+}
+
+// Largest increase of the running row max (log2 units) absorbed without
+// rescaling the accumulators: P values stay below 2^kLazy, far inside fp32 and
+// bf16 range, and the rescale runs only when some row of the wave exceeds it.
+constexpr float kLazy = 8.0f;
+
+// One 64-key tile for the wave's 32 query rows: S^T = K Q^T, online softmax
+// (max on raw scores, c > 0), O^T += V^T P^T.  Keys >= k_end are masked on
+// the (wave-uniform) tail tile only.
+template <typename T, int D>
+__device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
+                                         const typename Mfma<T>::v8 (&qf)[D / 16],
+                                         f32x16 (&acc)[D / 32], float &m_run, float &l_part,
+                                         float c, int kbase, int k_end, int lane) {
+  using M = Mfma<T>;
+  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int KS = D + kKPad;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  f32x16 s[2];
 #pragma unroll
-  for (int i = 0; i < TileRegs<D>::kVPer; ++i) {
-    const int qi = tid + 256 * i;
-    if (qi >= TileRegs<D>::kVQuads) continue;
-    const int kq = qi / CPR, dc = qi % CPR;
+  for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u32x2 w;
-      w[0] = half_of(r.vq[i][0], e) | (half_of(r.vq[i][1], e) << 16);
-      w[1] = half_of(r.vq[i][2], e) | (half_of(r.vq[i][3], e) << 16);
-      *reinterpret_cast<u32x2 *>(vt + (dc * 8 + e) * VS + kq * 4) = w;
+    for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const u32x4 a =
+          *reinterpret_cast<const u32x4 *>(ks + (kt * 32 + lrow) * KS + cc * 16 + lhalf * 8);
+      s[kt] = M::mma(as_v8<T>(a), qf[cc], s[kt]);
     }
   }
+  if (kbase + kBN > k_end) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (kbase + kt * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k_end) s[kt][r] = kNegInf;
+  }
+  float mx = kNegInf;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+  if (wave_any(mx > m_run + kLazy)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_part *= alpha;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+  }
+  float psum = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(__builtin_fmaf(s[kt][r], c, -m_run));
+      s[kt][r] = p;
+      psum += p;
+    }
+  l_part += psum;
+  typename M::v8 pb[2][2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) pb[kt][mm] = pack8<T>(s[kt], mm * 8);
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm)
+        acc[dt] = M::mma(tr_operand<T>(vs, KS, kt * 32 + mm * 16, dt * 32, lane), pb[kt][mm],
+                         acc[dt]);
 }
 
 template <typename T, int D>
@@ -100,7 +157,6 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
   using M = Mfma<T>;
   constexpr int NC = D / 16;   // 16-wide d chunks (S^T reduction)
   constexpr int ND = D / 32;   // 32-row d tiles of O^T
-  constexpr int KS = D + kKPad, VS = kBN + kVPad;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
@@ -113,15 +169,21 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
   const bool row_ok = qrow < q1;
   const bool wave_active = q0 + wave * 32 < q1;
 
-  // Q^T fragments (B operand): rows past q1 are zero.
+  // Q^T fragments (B operand): rows past q1 are zero.  A negative softmax
+  // scale is folded into Q (sign flips are exact) so c > 0 below.
+  const uint32_t qsign = c < 0.f ? 0x80008000u : 0u;
+  c = fabsf(c);
   typename M::v8 qf[NC];
+  {
+    const rsrc_t rq = make_rsrc(q + ((int64_t)q0 * H + h) * D, (int64_t)(q1 - q0) * H * D * 2);
+    const int lr = wave * 32 + lrow;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (row_ok)
-      val = *reinterpret_cast<const u32x4 *>(q + ((int64_t)qrow * H + h) * D + cc * 16 +
-                                              lhalf * 8);
-    qf[cc] = as_v8<T>(val);
+    for (int cc = 0; cc < NC; ++cc) {
+      u32x4 val = buf_load16(rq, (lr * H) * D * 2 + cc * 32 + lhalf * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) val[w] ^= qsign;
+      qf[cc] = as_v8<T>(val);
+    }
   }
 
   f32x16 acc[ND];
@@ -143,74 +205,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
     const int kbase = k0 + j * kBN;
     if (j + 1 < nt) load_tile<T, D>(regs, k, v, kbase + kBN, k1, H, h, tid);
     const T *ks = smem + (j & 1) * FwdSmem<D>::kBuf;
-    const T *vt = ks + FwdSmem<D>::kKs;
-    if (wave_active) {
-      // S^T = K Q^T for two 32-key sub-tiles.
-      f32x16 s[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < NC; ++cc) {
-          const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + (kt * 32 + lrow) * KS +
-                                                           cc * 16 + lhalf * 8);
-          s[kt] = M::mma(as_v8<T>(a), qf[cc], s[kt]);
-        }
-      }
-      // scale into the log2 domain, mask the key tail, row max
-      const bool tail = kbase + kBN > k1;
-      float mx = kNegInf;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float t = s[kt][r] * c;
-          if (tail) {
-            const int key = kbase + kt * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-            if (key >= k1) t = kNegInf;
-          }
-          s[kt][r] = t;
-          mx = fmaxf(mx, t);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(s[kt][r] - m_new);
-          s[kt][r] = p;
-          psum += p;
-        }
-      l_part = l_part * alpha + psum;
-#pragma unroll
-      for (int i = 0; i < ND; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
-      // O^T += V^T P^T
-      typename M::v8 pb[2][2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) pb[kt][mm] = pack8<T>(s[kt], mm * 8);
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const T *vrow = vt + (dt * 32 + lrow) * VS + lhalf * 4;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int mm = 0; mm < 2; ++mm) {
-            const int kk = kt * 32 + mm * 16;
-            const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow + kk);
-            const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + kk + 8);
-            acc[dt] = M::mma(as_v8<T>(join(lo, hi)), pb[kt][mm], acc[dt]);
-          }
-      }
-    }
+    const T *vs = ks + FwdSmem<D>::kKs;
+    if (wave_active) fwd_tile<T, D>(ks, vs, qf, acc, m_run, l_part, c, kbase, k1, lane);
     if (j + 1 < nt) {
       T *nks = smem + ((j + 1) & 1) * FwdSmem<D>::kBuf;
       store_tile<T, D>(regs, nks, nks + FwdSmem<D>::kKs, tid);

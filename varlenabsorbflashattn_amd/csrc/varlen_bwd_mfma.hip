@@ -4,7 +4,8 @@
 // from the forward's log2-domain LSE (fa/kernels.py:233-494):
 //   * dK/dV, key-major: a workgroup owns 128 keys of one head (32 per wave,
 //     K and V held in registers as MFMA operands) and walks the segment's
-//     queries in blocks of 32 staged in LDS (row-major and transposed):
+//     queries in blocks of 32 staged row-major in LDS (the transposed
+//     operands Q^T, dO^T come from ds_read_b64_tr_b16):
 //       S = Q K^T, dP = dO V^T, dS = P (dP - delta),
 //       dV^T += dO^T P,  dK^T += Q^T dS           (4 products per block)
 //   * dQ, query-major over the forward's plan items (including split-K
@@ -19,86 +20,51 @@ namespace vafa {
 namespace {
 
 constexpr int kRB = 32;  // rows per staged block (queries for dK/dV, keys for dQ)
-constexpr int kTP = 4;   // transposed-row padding (elements)
 
-// Registers of a [kRB x D] row block staged as 4-row x 8-column quads.
+// A [kRB x D] block of a [T, H, D] tensor staged through registers: 16-byte
+// chunks, rows past the buffer range read as zero.
 template <int D, int NT>
-struct Quads {
-  static constexpr int kQuads = (kRB / 4) * (D / 8);
-  static constexpr int kPer = (kQuads + NT - 1) / NT;
-  u32x4 v[kPer][4];
+struct Rows {
+  static constexpr int kChunks = kRB * D / 8;
+  static constexpr int kPer = (kChunks + NT - 1) / NT;
+  u32x4 v[kPer];
 };
 
 template <typename T, int D, int NT>
-__device__ __forceinline__ void load_quads(Quads<D, NT> &s, const T *__restrict__ src, int r0,
-                                           int r_end, int H, int h, int t) {
+__device__ __forceinline__ void load_rows(Rows<D, NT> &s, const T *__restrict__ src, int r0,
+                                          int r_end, int H, int h, int t) {
   constexpr int CPR = D / 8;
+  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
+  const rsrc_t rs = make_rsrc(src + (int64_t)r0 * H * D, (int64_t)rows * H * D * 2);
 #pragma unroll
-  for (int i = 0; i < Quads<D, NT>::kPer; ++i) {
-    const int qi = t + NT * i;
-    const int rq = qi / CPR, dc = qi % CPR;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = r0 + rq * 4 + e;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (qi < Quads<D, NT>::kQuads && row < r_end)
-        val = *reinterpret_cast<const u32x4 *>(src + ((int64_t)row * H + h) * D + dc * 8);
-      s.v[i][e] = val;
-    }
+  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
+    const int ci = t + NT * i;
+    const int row = ci < Rows<D, NT>::kChunks ? ci / CPR : kRB;
+    s.v[i] = buf_load16(rs, (row * H + h) * D * 2 + (ci % CPR) * 16);
   }
 }
 
-// Row-major copy (stride RS) and/or transposed copy (stride TS) into LDS.
 template <typename T, int D, int NT>
-__device__ __forceinline__ void store_quads(const Quads<D, NT> &s, T *rm, int RS, T *tr, int TS,
-                                            int t) {
+__device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int RS, int t) {
   constexpr int CPR = D / 8;
 #pragma unroll
-  for (int i = 0; i < Quads<D, NT>::kPer; ++i) {
-    const int qi = t + NT * i;
-    if (qi >= Quads<D, NT>::kQuads) continue;
-    const int rq = qi / CPR, dc = qi % CPR;
-    if (rm != nullptr) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        *reinterpret_cast<u32x4 *>(rm + (rq * 4 + e) * RS + dc * 8) = s.v[i][e];
-    }
-    if (tr != nullptr) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        w[0] = half_of(s.v[i][0], e) | (half_of(s.v[i][1], e) << 16);
-        w[1] = half_of(s.v[i][2], e) | (half_of(s.v[i][3], e) << 16);
-        *reinterpret_cast<u32x2 *>(tr + (dc * 8 + e) * TS + rq * 4) = w;
-      }
-    }
+  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
+    const int ci = t + NT * i;
+    if (ci < Rows<D, NT>::kChunks)
+      *reinterpret_cast<u32x4 *>(dst + (ci / CPR) * RS + (ci % CPR) * 8) = s.v[i];
   }
-}
-
-// A operand of a transposed product over a 32-row block: lane (lrow, lhalf)
-// needs rows 16m + lhalf*4 + {0..3} and 16m + 8 + lhalf*4 + {0..3} of column
-// `col` from a transposed LDS tile (row = column index, stride TS).
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::v8 tr_operand_t(const T *tr, int TS, int col, int m,
-                                                           int lhalf) {
-  const T *p = tr + col * TS + m * 16 + lhalf * 4;
-  const u32x2 lo = *reinterpret_cast<const u32x2 *>(p);
-  const u32x2 hi = *reinterpret_cast<const u32x2 *>(p + 8);
-  return as_v8<T>(join(lo, hi));
 }
 
 template <int D>
 struct DkvSmem {
-  static constexpr int RS = D + 8, TS = kRB + kTP;
-  static constexpr int kQs = kRB * RS;          // Q row-major
-  static constexpr int kQt = D * TS;            // Q transposed
-  static constexpr int kElems = 2 * (kQs + kQt);  // Q and dO, both layouts
-  static constexpr int kBufBytes = kElems * 2 + 2 * kRB * 4;  // + LSE and delta
+  static constexpr int RS = D + 8;
+  static constexpr int kQs = kRB * RS;                        // Q (or dO) row-major
+  static constexpr int kBufBytes = 2 * kQs * 2 + 2 * kRB * 4;  // Q, dO, LSE, delta
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
+__global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
@@ -118,16 +84,16 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
   const bool wave_active = k0 + wave * 32 < k1;
 
   typename M::v8 kf[NC], vf[NC];
+  {
+    const int nk = k1 - k0;
+    const rsrc_t rk = make_rsrc(k + (int64_t)k0 * H * D, (int64_t)nk * H * D * 2);
+    const rsrc_t rv = make_rsrc(v + (int64_t)k0 * H * D, (int64_t)nk * H * D * 2);
+    const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (key_ok) {
-      const int64_t off = ((int64_t)key * H + h) * D + cc * 16 + lhalf * 8;
-      a = *reinterpret_cast<const u32x4 *>(k + off);
-      b = *reinterpret_cast<const u32x4 *>(v + off);
+    for (int cc = 0; cc < NC; ++cc) {
+      kf[cc] = as_v8<T>(buf_load16(rk, off + cc * 32));
+      vf[cc] = as_v8<T>(buf_load16(rv, off + cc * 32));
     }
-    kf[cc] = as_v8<T>(a);
-    vf[cc] = as_v8<T>(b);
   }
   f32x16 adk[ND], adv[ND];
 #pragma unroll
@@ -140,10 +106,10 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
   const bool stage_q = tid < 128;
   const int st = tid & 127;
   const T *src = stage_q ? q : dout;
-  Quads<D, 128> stg;
+  Rows<D, 128> stg;
   float st_lse = 0.f, st_dl = 0.f;
   auto fetch = [&](int qb) {
-    load_quads<T, D, 128>(stg, src, qb, q1, H, h, st);
+    load_rows<T, D, 128>(stg, src, qb, q1, H, h, st);
     if (tid < kRB) {
       const int row = qb + tid;
       st_lse = row < q1 ? lse[(int64_t)row * H + h] : __builtin_inff();
@@ -153,14 +119,8 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
   auto put = [&](int buf) {
     unsigned char *base = smem_raw + buf * S::kBufBytes;
     T *qs = reinterpret_cast<T *>(base);
-    T *qt = qs + S::kQs;
-    T *ds = qt + S::kQt;
-    T *dt = ds + S::kQs;
-    float *ls = reinterpret_cast<float *>(base + S::kElems * 2);
-    if (stage_q)
-      store_quads<T, D, 128>(stg, qs, S::RS, qt, S::TS, st);
-    else
-      store_quads<T, D, 128>(stg, ds, S::RS, dt, S::TS, st);
+    store_rows<T, D, 128>(stg, stage_q ? qs : qs + S::kQs, S::RS, st);
+    float *ls = reinterpret_cast<float *>(base + 2 * S::kQs * 2);
     if (tid < kRB) {
       ls[tid] = st_lse;
       ls[kRB + tid] = st_dl;
@@ -178,10 +138,8 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
     if (wave_active) {
       const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
       const T *qs = reinterpret_cast<const T *>(base);
-      const T *qt = qs + S::kQs;
-      const T *ds_ = qt + S::kQt;
-      const T *dt_ = ds_ + S::kQs;
-      const float *ls = reinterpret_cast<const float *>(base + S::kElems * 2);
+      const T *ds_ = qs + S::kQs;
+      const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
@@ -199,7 +157,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = g * 4 + e;
-          const float p = key_ok ? fast_exp2(s[r] * c - L[e]) : 0.f;
+          const float p = key_ok ? fast_exp2(__builtin_fmaf(s[r], c, -L[e])) : 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - Dl[e]);
         }
@@ -211,14 +169,14 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
         sb[mm] = pack8<T>(dp, mm * 8);
       }
 #pragma unroll
-      for (int dtile = 0; dtile < ND; ++dtile) {
-        const int col = dtile * 32 + lrow;
+      for (int dtile = 0; dtile < ND; ++dtile)
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
-          adv[dtile] = M::mma(tr_operand_t<T>(dt_, S::TS, col, mm, lhalf), pb[mm], adv[dtile]);
-          adk[dtile] = M::mma(tr_operand_t<T>(qt, S::TS, col, mm, lhalf), sb[mm], adk[dtile]);
+          adv[dtile] = M::mma(tr_operand<T>(ds_, S::RS, mm * 16, dtile * 32, lane), pb[mm],
+                              adv[dtile]);
+          adk[dtile] = M::mma(tr_operand<T>(qs, S::RS, mm * 16, dtile * 32, lane), sb[mm],
+                              adk[dtile]);
         }
-      }
     }
     if (j + 1 < nblk) put((j + 1) & 1);
     __syncthreads();
@@ -246,9 +204,9 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void varlen_dkv_kernel(
 
 template <int D>
 struct DqSmem {
-  static constexpr int RS = D + 8, TS = kRB + kTP;
-  static constexpr int kKs = kRB * RS, kKt = D * TS, kVs = kRB * RS;
-  static constexpr int kBuf = kKs + kKt + kVs;
+  static constexpr int RS = D + 8;
+  static constexpr int kKs = kRB * RS;
+  static constexpr int kBuf = 2 * kKs;  // K and V row-major
   static constexpr int kBytes = 2 * kBuf * 2;
 };
 
@@ -274,16 +232,16 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   const bool wave_active = q0 + wave * 32 < q1;
 
   typename M::v8 qf[NC], dof[NC];
+  {
+    const int64_t nb = (int64_t)(q1 - q0) * H * D * 2;
+    const rsrc_t rq = make_rsrc(q + (int64_t)q0 * H * D, nb);
+    const rsrc_t rd = make_rsrc(dout + (int64_t)q0 * H * D, nb);
+    const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (row_ok) {
-      const int64_t off = ((int64_t)qrow * H + h) * D + cc * 16 + lhalf * 8;
-      a = *reinterpret_cast<const u32x4 *>(q + off);
-      b = *reinterpret_cast<const u32x4 *>(dout + off);
+    for (int cc = 0; cc < NC; ++cc) {
+      qf[cc] = as_v8<T>(buf_load16(rq, off + cc * 32));
+      dof[cc] = as_v8<T>(buf_load16(rd, off + cc * 32));
     }
-    qf[cc] = as_v8<T>(a);
-    dof[cc] = as_v8<T>(b);
   }
   const float Lr = row_ok ? lse[(int64_t)qrow * H + h] : __builtin_inff();
   const float Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
@@ -293,32 +251,27 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-  // threads 0..127 stage K (row-major + transposed), 128..255 stage V (row-major)
+  // threads 0..127 stage K, 128..255 stage V (both row-major)
   const bool stage_k = tid < 128;
   const int st = tid & 127;
-  Quads<D, 128> stg;
+  const T *src = stage_k ? k : v;
+  Rows<D, 128> stg;
   const int nblk = (k1 - k0 + kRB - 1) / kRB;
   auto put = [&](int buf) {
     T *ks = smem + buf * S::kBuf;
-    T *kt = ks + S::kKs;
-    T *vs = kt + S::kKt;
-    if (stage_k)
-      store_quads<T, D, 128>(stg, ks, S::RS, kt, S::TS, st);
-    else
-      store_quads<T, D, 128>(stg, vs, S::RS, nullptr, 0, st);
+    store_rows<T, D, 128>(stg, stage_k ? ks : ks + S::kKs, S::RS, st);
   };
   if (nblk > 0) {
-    load_quads<T, D, 128>(stg, stage_k ? k : v, k0, k1, H, h, st);
+    load_rows<T, D, 128>(stg, src, k0, k1, H, h, st);
     put(0);
   }
   __syncthreads();
   for (int j = 0; j < nblk; ++j) {
     const int kb = k0 + j * kRB;
-    if (j + 1 < nblk) load_quads<T, D, 128>(stg, stage_k ? k : v, kb + kRB, k1, H, h, st);
+    if (j + 1 < nblk) load_rows<T, D, 128>(stg, src, kb + kRB, k1, H, h, st);
     if (wave_active) {
       const T *ks = smem + (j & 1) * S::kBuf;
-      const T *kt = ks + S::kKs;
-      const T *vs = kt + S::kKt;
+      const T *vs = ks + S::kKs;
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
@@ -329,23 +282,25 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
         const u32x4 b = *reinterpret_cast<const u32x4 *>(vs + lrow * S::RS + cc * 16 + lhalf * 8);
         dp = M::mma(as_v8<T>(b), dof[cc], dp);
       }
-      const bool tail = kb + kRB > k1;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(s[r] * c - Lr);
-        if (tail && kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) p = 0.f;
+        const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lr));
         dp[r] = p * (dp[r] - Dr);
+      }
+      if (kb + kRB > k1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) dp[r] = 0.f;
       }
       typename M::v8 sb[2];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) sb[mm] = pack8<T>(dp, mm * 8);
 #pragma unroll
-      for (int dtile = 0; dtile < ND; ++dtile) {
-        const int col = dtile * 32 + lrow;
+      for (int dtile = 0; dtile < ND; ++dtile)
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          acc[dtile] = M::mma(tr_operand_t<T>(kt, S::TS, col, mm, lhalf), sb[mm], acc[dtile]);
-      }
+          acc[dtile] = M::mma(tr_operand<T>(ks, S::RS, mm * 16, dtile * 32, lane), sb[mm],
+                              acc[dtile]);
     }
     if (j + 1 < nblk) put((j + 1) & 1);
     __syncthreads();

@@ -95,8 +95,12 @@ def bench_varlen_c3(iters):
 
 
 def bench_absorb(case, iters):
+    """Inner absorb forward on precomputed u, through the reference's hot-path
+    contract: prepare_target_attn_indices once, then validate=False calls
+    (ta/interface.py:125-138) -- no host round trip inside the timed loop."""
     import torch
-    from varlenabsorbflashattn_amd import target_attn_inner, workloads as W
+    from varlenabsorbflashattn_amd import prepare_target_attn_indices, target_attn_inner
+    from varlenabsorbflashattn_amd import workloads as W
     from varlenabsorbflashattn_amd.absorb import _project_u
     dev = torch.device("cuda:0")
     q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev)
@@ -104,10 +108,11 @@ def bench_absorb(case, iters):
     with torch.no_grad():
         u = _project_u(q_raw, W_Q, W_K).contiguous()
     scale = 1.0 / math.sqrt(case.D_H)
+    qi, ki = prepare_target_attn_indices(cq, ck)
 
     def fwd():
         with torch.no_grad():
-            target_attn_inner(u, X, W_V, cq, ck, scale)
+            target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
 
     fwd()
     ms = time_region(fwd, iters)

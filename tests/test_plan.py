@@ -193,9 +193,21 @@ def check_absorb_plan(q_lens, k_lens, H=8):
     TT = p.info.q_tile
     assert TT * H <= 128
     cover = {}
-    for t0, t1, k0, k1, pb, seg, s, ns in p.section("fwd").tolist():
+    fwd = p.section("fwd").tolist()
+    slot_of = {}
+    for pos, (t0, t1, k0, k1, pb, seg, s, ns) in enumerate(fwd):
+        if seg == -1:  # no-op slot of the XCD-aware layout
+            assert t0 == t1
+            continue
         assert cq[seg] <= t0 < t1 <= cq[seg + 1] and t1 - t0 <= TT
         cover.setdefault((t0, t1), []).append((k0, k1))
+        # all tiles reading one key range run on one XCD (grid slot mod 8)
+        slot_of.setdefault((seg, k0, k1), set()).add(pos % 8)
+    assert all(len(v) == 1 for v in slot_of.values())
+    for ranges in cover.values():
+        ranges.sort()
+        for a, b in zip(ranges, ranges[1:]):
+            assert a[1] == b[0]
     qt = p.section("qt")
     n_tiles = sum(-(-int(L) // TT) for L in q_lens)
     assert len(qt) == n_tiles == len(cover)

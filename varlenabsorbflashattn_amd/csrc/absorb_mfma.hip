@@ -1,13 +1,15 @@
 // Absorbed ragged target attention forward on gfx950 matrix cores
 // (replaces ta/kernels.py:185-284, the default "alpha" forward).
 //
-// One workgroup = 4 waves owns up to 128 (token, head) rows of one sample --
-// all H heads of 128/H consecutive tokens, token-major, so the rows are one
-// contiguous slab of u -- and one key range.  Each 32-key tile of raw X is
-// read from HBM once per workgroup (not once per head) and staged in LDS both
-// row-major (A operand of S^T = X U^T) and transposed (A operand of
-// aX^T += X^T P^T).  After the key loop aX/l is rounded to the input dtype,
-// regrouped head-major in LDS and projected by W_V with 16x16x32 MFMAs.
+// One workgroup = 2 waves owns up to 64 (token, head) rows of one sample --
+// all H heads of 64/H consecutive tokens, token-major, so the rows are one
+// contiguous slab of u -- and one key range.  Raw X is streamed once per
+// workgroup (not once per head) through a 3-deep ring of 32-key LDS tiles
+// filled by buffer_load ... lds, one instruction per padded row (no staging
+// registers; rows past the key range arrive as zeros).  Per tile each wave issues S^T = X U^T (X rows as the A
+// operand) and aX^T += X^T P^T (X^T from ds_read_b64_tr_b16), with the online
+// softmax in the log2 domain.  After the key loop aX/l is rounded to the input
+// dtype, regrouped head-major in LDS and projected by W_V (16x16x32 MFMAs).
 #include "kernels.h"
 #include "mfma.h"
 
@@ -15,22 +17,21 @@ namespace vafa {
 
 namespace {
 
-constexpr int kRows = kAbsorbRows;  // 128 rows per workgroup
-constexpr int kBK = 32;             // keys per LDS tile
-constexpr int kMaxF = 256;          // D_KV handled by this kernel (padded to 32)
+constexpr int kWaves = kAbsorbRows / 32;  // 2 waves x 32 rows
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBK = 32;                   // keys per LDS tile
+constexpr int kNBuf = 3;                  // LDS ring depth
+constexpr int kMaxF = 256;                // D_KV handled by this kernel (padded to 32)
 
 template <int FP>
 struct AbsSmem {
-  static constexpr int XS = FP + 8;   // row-major X stride
-  static constexpr int TS = kBK + 4;  // transposed X stride
-  static constexpr int kXs = kBK * XS, kXt = FP * TS;
-  static constexpr int kBuf = kXs + kXt;
-  static constexpr int kLoopBytes = 2 * kBuf * 2;
-  static constexpr int kEpiBytes = kRows * XS * 2;  // head-major aX rows
+  static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
+  static constexpr int XS = FP + 8;                  // padded row stride (elements)
+  static constexpr int kTile = kBK * XS;             // elements per tile
+  static constexpr int kLoopBytes = kNBuf * kTile * 2;
+  static constexpr int kEpiBytes = kAbsorbRows * XS * 2;
   static constexpr int kBytes = kLoopBytes > kEpiBytes ? kLoopBytes : kEpiBytes;
 };
-
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
 
 template <typename T>
 struct Mfma16;
@@ -62,8 +63,29 @@ __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__
   wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
 }
 
+// Issue the LDS-DMA loads of one 32-key tile: one instruction per X row,
+// lanes 0..CPR-1 each move one 16-byte chunk to the row's padded LDS slot
+// (keys past k_end and chunks past D_KV arrive as zeros).  Every wave issues
+// kBK / kWaves instructions per tile, which keeps vmcnt accounting uniform.
+template <typename T, int FP>
+__device__ __forceinline__ void issue_tile(const T *__restrict__ X, int kb, int k_end, int F,
+                                           T *tile, int wave, int lane) {
+  using S = AbsSmem<FP>;
+  const int rows = k_end - kb < kBK ? (k_end - kb > 0 ? k_end - kb : 0) : kBK;
+  const u32x4 rx = rsrc_words(X + (int64_t)kb * F, (int64_t)rows * F * 2);
+  const int off = lane < F / 8 ? lane * 16 : 0x7fffffff;
+  const uint32_t base = lds_addr(tile);
+  if (lane < S::CPR) {
+#pragma unroll
+    for (int n = 0; n < kBK / kWaves; ++n) {
+      const int r = wave * (kBK / kWaves) + n;
+      lds_dma16(rx, base + r * S::XS * 2, off + r * F * 2);
+    }
+  }
+}
+
 template <typename T, int FP, int DH>
-__global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
+__global__ __launch_bounds__(kThreads, 2) void absorb_fwd_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ wvt,
     T *__restrict__ O, float *__restrict__ lse, float *__restrict__ part_o,
     float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, int F, float c) {
@@ -71,29 +93,42 @@ __global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
   using S = AbsSmem<FP>;
   constexpr int NC = FP / 16;   // S^T reduction chunks
   constexpr int NF = FP / 32;   // aX^T row tiles
-  constexpr int CPR = FP / 8;   // 16-byte chunks per padded X row
+  constexpr int kPerWave = kBK / kWaves;  // DMA instructions per wave per tile
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
   const PlanItem it = load_item(items, blockIdx.x);
   const int t0 = it.v[0], t1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (t1 <= t0) return;  // no-op slot of the XCD-aware layout
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int nrows = (t1 - t0) * H;
   const int row = wave * 32 + lrow;  // local (token-major) row
   const bool row_ok = row < nrows;
   const bool wave_active = wave * 32 < nrows;
-  const int fchunks = F / 8;         // valid 16-byte chunks per X / u row
+  const int nt = (k1 - k0 + kBK - 1) / kBK;
+
+  // start the first kNBuf-1 tiles before anything else
+#pragma unroll
+  for (int b = 0; b < kNBuf - 1; ++b)
+    issue_tile<T, FP>(X, k0 + b * kBK, k1, F, smem + b * S::kTile, wave, lane);
 
   // U^T fragments (B operand of S^T = X U^T)
   typename M::v8 uf[NC];
-  const T *urow = u + ((int64_t)t0 * H + row) * F;
+  {
+    const rsrc_t ru = make_rsrc(u + (int64_t)t0 * H * F, (int64_t)nrows * F * 2);
+    const int fchunks = F / 8;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    const int ch = cc * 2 + lhalf;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (row_ok && ch < fchunks) val = *reinterpret_cast<const u32x4 *>(urow + ch * 8);
-    uf[cc] = as_v8<T>(val);
+    for (int cc = 0; cc < NC; ++cc) {
+      const int ch = cc * 2 + lhalf;
+      u32x4 w = buf_load16(ru, ch < fchunks ? row * F * 2 + ch * 16 : 0x7fffffff);
+      // pass through an empty asm: the compiler waits for the load here, in
+      // the prologue, instead of before every use inside the key loop (where
+      // its vmcnt waits would also drain the LDS-DMA prefetch)
+      asm volatile("" : "+v"(w));
+      uf[cc] = as_v8<T>(w);
+    }
   }
   f32x16 acc[NF];
 #pragma unroll
@@ -101,114 +136,82 @@ __global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   float m_run = kNegInf, l_part = 0.f;
-
-  // tile staging: 4-key x 8-feature quads, (kBK/4)*CPR of them
-  constexpr int kQuads = (kBK / 4) * CPR;
-  constexpr int kPer = (kQuads + 255) / 256;
-  u32x4 stg[kPer][4];
-  auto fetch = [&](int kb) {
+  const uint32_t usign = c < 0.f ? 0x80008000u : 0u;  // fold a negative scale into u
+  if (usign) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int qi = tid + 256 * i;
-      const int kq = qi / CPR, dc = qi % CPR;
+    for (int cc = 0; cc < NC; ++cc) {
+      u32x4 w = __builtin_bit_cast(u32x4, uf[cc]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = kb + kq * 4 + e;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (qi < kQuads && key < k1 && dc < fchunks)
-          val = *reinterpret_cast<const u32x4 *>(X + (int64_t)key * F + dc * 8);
-        stg[i][e] = val;
-      }
+      for (int e = 0; e < 4; ++e) w[e] ^= usign;
+      uf[cc] = as_v8<T>(w);
     }
-  };
-  auto put = [&](int buf) {
-    T *xs = smem + buf * S::kBuf;
-    T *xt = xs + S::kXs;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int qi = tid + 256 * i;
-      if (qi >= kQuads) continue;
-      const int kq = qi / CPR, dc = qi % CPR;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        *reinterpret_cast<u32x4 *>(xs + (kq * 4 + e) * S::XS + dc * 8) = stg[i][e];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        w[0] = half_of(stg[i][0], e) | (half_of(stg[i][1], e) << 16);
-        w[1] = half_of(stg[i][2], e) | (half_of(stg[i][3], e) << 16);
-        *reinterpret_cast<u32x2 *>(xt + (dc * 8 + e) * S::TS + kq * 4) = w;
-      }
-    }
-  };
-
-  const int nt = (k1 - k0 + kBK - 1) / kBK;
-  if (nt > 0) {
-    fetch(k0);
-    put(0);
   }
-  __syncthreads();
+  c = fabsf(c);
+
   for (int j = 0; j < nt; ++j) {
+    // tile j landed (later tiles may still be in flight), visible to all waves,
+    // and every wave is done with tile j-1 whose slot is refilled next
+    wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    __syncthreads();
+    issue_tile<T, FP>(X, k0 + (j + kNBuf - 1) * kBK, k1, F,
+                      smem + ((j + kNBuf - 1) % kNBuf) * S::kTile, wave, lane);
     const int kb = k0 + j * kBK;
-    if (j + 1 < nt) fetch(kb + kBK);
+    const T *xs = smem + (j % kNBuf) * S::kTile;
     if (wave_active) {
-      const T *xs = smem + (j & 1) * S::kBuf;
-      const T *xt = xs + S::kXs;
       f32x16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(xs + lrow * S::XS + cc * 16 + lhalf * 8);
+        const u32x4 a =
+            *reinterpret_cast<const u32x4 *>(xs + lrow * S::XS + cc * 16 + lhalf * 8);
         s = M::mma(as_v8<T>(a), uf[cc], s);
       }
-      const bool tail = kb + kBK > k1;
+      if (kb + kBK > k1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) s[r] = kNegInf;
+      }
       float mx = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float t = s[r] * c;
-        if (tail && kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) t = kNegInf;
-        s[r] = t;
-        mx = fmaxf(mx, t);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+      if (wave_any(mx > m_run + 8.0f)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_part *= alpha;
+#pragma unroll
+        for (int i = 0; i < NF; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
       float psum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[r] - m_new);
+        const float p = fast_exp2(__builtin_fmaf(s[r], c, -m_run));
         s[r] = p;
         psum += p;
       }
-      l_part = l_part * alpha + psum;
-#pragma unroll
-      for (int i = 0; i < NF; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+      l_part += psum;
       typename M::v8 pb[2];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) pb[mm] = pack8<T>(s, mm * 8);
+      // aX^T += X^T P^T with X^T read transposed out of the row-major tile
 #pragma unroll
-      for (int ft = 0; ft < NF; ++ft) {
-        const T *xrow = xt + (ft * 32 + lrow) * S::TS + lhalf * 4;
+      for (int ft = 0; ft < NF; ++ft)
 #pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          const u32x2 lo = *reinterpret_cast<const u32x2 *>(xrow + mm * 16);
-          const u32x2 hi = *reinterpret_cast<const u32x2 *>(xrow + mm * 16 + 8);
-          acc[ft] = M::mma(as_v8<T>(join(lo, hi)), pb[mm], acc[ft]);
-        }
-      }
+        for (int mm = 0; mm < 2; ++mm)
+          acc[ft] = M::mma(tr_operand<T>(xs, S::XS, mm * 16, ft * 32, lane), pb[mm], acc[ft]);
     }
-    if (j + 1 < nt) put((j + 1) & 1);
-    __syncthreads();
   }
+  wait_vmcnt<0>();
+  __syncthreads();
 
   // ---- epilogue: aX/l -> LDS (head-major rows, input dtype), then W_V ----
   const float l = l_part + __shfl_xor(l_part, 32, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int TT = kRows / H;               // tokens per workgroup
+  const int TT = kAbsorbRows / H;         // tokens per workgroup
   const int tl = row / H, hh = row % H;   // token / head of this lane's row
   if (row_ok && lhalf == 0) {
     const float lse_v = l > 0.f ? m_run + fast_log2(l) : kNegInf;
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
     else
       part_lse[(int64_t)(pbase + tl) * H + hh] = lse_v;
   }
-  T *axs = smem;  // [kRows][XS], row h*TT + t
+  T *axs = smem;  // [kAbsorbRows][XS], row h*TT + t
   if (wave_active) {
     T *dst = axs + (hh * TT + tl) * S::XS;
 #pragma unroll
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
   const int ntok = t1 - t0;
   const int tiles_per_head = (TT + 15) / 16;
   const int n_tiles = H * tiles_per_head * (DH / 16);
-  for (int tile = wave; tile < n_tiles; tile += 4) {
+  for (int tile = wave; tile < n_tiles; tile += kWaves) {
     const int dtile = tile % (DH / 16);
     const int tt = (tile / (DH / 16)) % tiles_per_head;
     const int h = tile / ((DH / 16) * tiles_per_head);
@@ -245,10 +248,11 @@ __global__ __launch_bounds__(256, 1) void absorb_fwd_kernel(
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
     const T *arow = axs + (h * TT + tt * 16 + l16) * S::XS + lq * 8;
     const T *brow = wvt + ((int64_t)h * DH + dtile * 16 + l16) * FP + lq * 8;
+    const bool a_ok = tt * 16 + l16 < TT;
 #pragma unroll
     for (int kc = 0; kc < FP / 32; ++kc) {
-      const u32x4 a = (tt * 16 + l16 < TT) ? *reinterpret_cast<const u32x4 *>(arow + kc * 32)
-                                          : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 a = a_ok ? *reinterpret_cast<const u32x4 *>(arow + kc * 32)
+                           : u32x4{0u, 0u, 0u, 0u};
       const u32x4 b = *reinterpret_cast<const u32x4 *>(brow + kc * 32);
       o = Mfma16<T>::mma(as_v8<T>(a), as_v8<T>(b), o);
     }
@@ -270,8 +274,8 @@ void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   const int smem = AbsSmem<FP>::kBytes;
   hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(256), smem,
-                     st, (const T *)a.u, (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o,
+  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(kThreads),
+                     smem, st, (const T *)a.u, (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o,
                      a.part_lse, a.items, a.H, a.F, a.scale * kLog2e);
 }
 
@@ -291,7 +295,7 @@ inline int padded_f(int F) { return (F + 31) / 32 * 32; }
 
 }  // namespace
 
-// The matrix-core path takes H | 128 with 128/H >= 16 tokens per workgroup,
+// The matrix-core path takes H | 64 with at least 8 tokens per workgroup,
 // D_KV a multiple of 8 that pads (to 32) onto one of the compiled widths,
 // and D_H in {16, 32, 64, 128}.
 template <typename T>
@@ -299,7 +303,7 @@ bool mfma_absorb_supported(int H, int F, int DH) {
   const int FP = padded_f(F);
   const bool f_ok = F % 8 == 0 && F <= kMaxF &&
                     (FP == 64 || FP == 128 || FP == 192 || FP == 224 || FP == 256);
-  const bool h_ok = H >= 1 && H <= 8 && (kRows % H) == 0;
+  const bool h_ok = H >= 1 && H <= 8 && (kAbsorbRows % H) == 0;
   const bool d_ok = DH == 16 || DH == 32 || DH == 64 || DH == 128;
   return f_ok && h_ok && d_ok;
 }

@@ -64,6 +64,49 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
 
+// 16-byte LDS-DMA load: lane l's 16 bytes from `rsrc` at byte offset `voff`
+// land at LDS address lds_base + 16*l (out-of-range offsets write zeros).
+// Written as inline asm so that the compiler's automatic waits do not treat
+// every later LDS read as dependent on it; callers order it with explicit
+// s_waitcnt vmcnt(N) + barrier.
+// Raw buffer descriptor words (base, stride 0, num_records, gfx9 flags) for
+// use in inline asm.
+__device__ __forceinline__ u32x4 rsrc_words(const void *base, int64_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 r;
+  r[0] = (uint32_t)a;
+  r[1] = (uint32_t)(a >> 32) & 0xffffu;
+  r[2] = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : bytes));
+  r[3] = 0x00020000u;
+  return r;
+}
+
+__device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t lds_base, int32_t voff) {
+  // (an ext_vector_type operand is what binds to an SGPR quad under "s")
+  typedef uint32_t sgpr4 __attribute__((ext_vector_type(4)));
+  sgpr4 q;
+  q.x = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[0]);
+  q.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[1]);
+  q.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[2]);
+  q.w = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[3]);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(q)
+               : "memory", "m0");
+}
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+template <typename P>
+__device__ __forceinline__ uint32_t lds_addr(const P *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) P *)(p);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Wave-uniform "any lane" vote.
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 

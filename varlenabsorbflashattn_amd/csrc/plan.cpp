@@ -73,6 +73,49 @@ void sort_lpt(std::vector<Item> &items) {
                    [](const Item &a, const Item &b) { return a.cost > b.cost; });
 }
 
+// Items that read the same key range (same segment and split, different
+// query tiles) form a bundle.  Bundles are assigned longest-first to the
+// least-loaded XCD and the grid is laid out in rounds of kXcds slots, slot x
+// running on XCD x, so the members of a bundle run back to back on one XCD
+// and share its L2.  Empty slots are padded with no-op items (t0 == t1).
+std::vector<Item> xcd_bundle(const std::vector<Item> &items) {
+  std::vector<std::vector<Item>> bundles;
+  std::vector<int64_t> cost;
+  for (const Item &it : items) {
+    // split items of one tile are emitted consecutively per (segment, split)
+    bool joined = false;
+    if (!bundles.empty()) {
+      const Item &h = bundles.back().front();
+      joined = h.v[5] == it.v[5] && h.v[6] == it.v[6] && h.v[2] == it.v[2] && h.v[3] == it.v[3];
+    }
+    if (!joined) {
+      bundles.emplace_back();
+      cost.push_back(0);
+    }
+    bundles.back().push_back(it);
+    cost.back() += it.cost;
+  }
+  std::vector<size_t> order(bundles.size());
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](size_t a, size_t b) { return cost[a] > cost[b]; });
+  std::vector<std::vector<Item>> q(kXcds);
+  std::vector<int64_t> load(kXcds, 0);
+  for (size_t b : order) {
+    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    for (const Item &it : bundles[b]) q[x].push_back(it);
+    load[x] += cost[b];
+  }
+  size_t rounds = 0;
+  for (const auto &v : q) rounds = std::max(rounds, v.size());
+  std::vector<Item> out;
+  out.reserve(rounds * kXcds);
+  const Item noop{{0, 0, 0, 0, -1, -1, 0, 1}, 0};
+  for (size_t r = 0; r < rounds; ++r)
+    for (int x = 0; x < kXcds; ++x) out.push_back(r < q[x].size() ? q[x][r] : noop);
+  return out;
+}
+
 int emit(const std::vector<Item> &sec0, const std::vector<Item> &sec1,
          const std::vector<Item> &sec2, const std::vector<Item> &sec3, int32_t *plan,
          int64_t cap, vafa_plan_info *info) {
@@ -250,10 +293,13 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
 }
 
 // Absorb plan.  Query rows are (token, head) pairs; one item covers whole
-// tokens [t0, t1) with (t1 - t0) * H <= kAbsorbRows.
+// tokens [t0, t1) with (t1 - t0) * H <= kAbsorbRows.  A segment's tiles share
+// one split of its key range.
 //   fwd section : {t0, t1, k0, k1, pbase, seg, split, nsplit}; split items
 //                 write projected partial rows pbase + r (r < t1-t0), each
-//                 holding H x D_H fp32 outputs and H log2-domain LSEs.
+//                 holding H x D_H fp32 outputs and H log2-domain LSEs.  The
+//                 section is laid out XCD-aware (see xcd_bundle) and may hold
+//                 no-op items {0, 0, 0, 0, -1, -1, 0, 1}.
 //   comb section: {t0, t1, pbase, nsplit, seg, 0, 0, 0}.
 //   kv section  : {k0, k1, t0, t1, seg, 0, 0, 0} key tiles for dX with the
 //                 segment's whole token range [t0, t1).
@@ -284,30 +330,36 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   for (int64_t s = 0; s + 1 < n1; ++s) {
     const int64_t q0 = cu_q[s], q1 = cu_q[s + 1], k0 = cu_k[s], k1 = cu_k[s + 1];
     const int64_t lq = q1 - q0, lk = k1 - k0;
+    // one split decision per segment (its tiles share the key ranges)
+    int64_t ns = 1, chunk = lk;
+    if (lq > 0) key_split(std::min<int64_t>(lq, TT) * H, lk, pol, &ns, &chunk);
+    max_split = std::max(max_split, ns);
+    const int64_t seg_prow = prow;
     for (int64_t t = q0; t < q1; t += TT) {
       const int64_t te = std::min(t + TT, q1), ntok = te - t;
-      int64_t ns, chunk;
-      key_split(ntok * H, lk, pol, &ns, &chunk);
-      max_split = std::max(max_split, ns);
       const int64_t row_cost = round_up(ntok * H, 32);
       qt.push_back(Item{{(int32_t)t, (int32_t)te, (int32_t)k0, (int32_t)k1, -1, (int32_t)s, 0, 1},
                         (lk + pol.item_overhead) * row_cost});
-      if (ns <= 1) {
-        Item it{{(int32_t)t, (int32_t)te, (int32_t)k0, (int32_t)k1, -1, (int32_t)s, 0, 1},
-                (lk + pol.item_overhead) * row_cost};
-        fwd.push_back(it);
-        continue;
+      if (ns > 1) {
+        Item c{{(int32_t)t, (int32_t)te, (int32_t)prow, (int32_t)ns, (int32_t)s, 0, 0, 0}, 0};
+        comb.push_back(c);
+        prow += ns * ntok;
       }
-      Item c{{(int32_t)t, (int32_t)te, (int32_t)prow, (int32_t)ns, (int32_t)s, 0, 0, 0}, 0};
-      comb.push_back(c);
-      for (int64_t j = 0; j < ns; ++j) {
-        const int64_t a = k0 + j * chunk, b = std::min(k1, a + chunk);
-        Item it{{(int32_t)t, (int32_t)te, (int32_t)a, (int32_t)b, (int32_t)(prow + j * ntok),
-                 (int32_t)s, (int32_t)j, (int32_t)ns},
-                ((b - a) + pol.item_overhead) * row_cost};
-        fwd.push_back(it);
+    }
+    // forward items: split-major so that the tiles of one key range are adjacent
+    for (int64_t j = 0; j < ns; ++j) {
+      const int64_t a = ns > 1 ? k0 + j * chunk : k0;
+      const int64_t b = ns > 1 ? std::min(k1, a + chunk) : k1;
+      int64_t tile_prow = seg_prow;
+      for (int64_t t = q0; t < q1; t += TT) {
+        const int64_t te = std::min(t + TT, q1), ntok = te - t;
+        const int64_t row_cost = round_up(ntok * H, 32);
+        const int32_t pb = ns > 1 ? (int32_t)(tile_prow + j * ntok) : -1;
+        fwd.push_back(Item{{(int32_t)t, (int32_t)te, (int32_t)a, (int32_t)b, pb, (int32_t)s,
+                            (int32_t)j, (int32_t)ns},
+                           ((b - a) + pol.item_overhead) * row_cost});
+        tile_prow += ns * ntok;
       }
-      prow += ns * ntok;
     }
     for (int64_t k = k0; k < k1; k += BK) {
       const int64_t ke = std::min(k + BK, k1);
@@ -316,7 +368,7 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
       kv.push_back(it);
     }
   }
-  sort_lpt(fwd);
+  fwd = xcd_bundle(fwd);
   sort_lpt(kv);
   sort_lpt(qt);
   info->n_part_rows = prow;

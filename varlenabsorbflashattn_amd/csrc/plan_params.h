@@ -10,7 +10,7 @@ constexpr int kVarlenQTile = 128;
 constexpr int kVarlenKTile = 128;
 // Absorb: a forward workgroup covers up to kAbsorbRows (token, head) rows;
 // a dX workgroup covers kAbsorbKTile keys.
-constexpr int kAbsorbRows = 128;
+constexpr int kAbsorbRows = 64;
 constexpr int kAbsorbKTile = 64;
 
 struct SplitPolicy {
@@ -26,5 +26,9 @@ struct SplitPolicy {
 
 constexpr SplitPolicy kVarlenPolicy{16, 1024, 2048, 4, 16, 4096, 4096, 64, 64};
 constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 2048, 1024, 64, 32};
+
+// Workgroups are dispatched round-robin over this many XCDs (one L2 each):
+// workgroup i runs on XCD i % kXcds.
+constexpr int kXcds = 8;
 
 }  // namespace vafa

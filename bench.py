@@ -71,8 +71,15 @@ def bench_varlen_c2(steps, warmup):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     fwd_ms = time_region(fwd, max(steps, 3))
+    # dominant kernel: dK/dV, timed alone with HIP events on the launch stream
+    from varlenabsorbflashattn_amd.varlen import BackwardStages
+    stages = BackwardStages(q.detach(), k.detach(), v.detach(), do, cu, cu)
+    stages.run(0)
+    stages.run(2)
+    dkv_ms = time_region(lambda: stages.run(2), max(steps, 3))
+    del stages
     flops = case.flops_fwd + case.flops_bwd
-    return case, ms, fwd_ms, flops
+    return case, ms, fwd_ms, flops, dkv_ms
 
 
 def bench_varlen_c3(iters):
@@ -121,6 +128,17 @@ def bench_absorb(case, iters):
     return ms
 
 
+def roofline_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (profiles/roofline_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "roofline_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("varlen_dkv_kernel", {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(budget_s=15.0):
     """Oracle (numpy fp32) fwd+bwd on the shortest-first prefix of C2's segments
     that fits the time budget; reported as TFLOP/s of that sample."""
@@ -153,6 +171,28 @@ def cpu_baseline(budget_s=15.0):
                       f"{t_used:.1f} s"}
 
 
+def run_only(which, steps, warmup):
+    """One configuration, for per-kernel profiling runs."""
+    from varlenabsorbflashattn_amd import workloads as W
+    if which == "copy":
+        # calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE: a 1 GiB device copy
+        import torch
+        x = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
+        y = torch.empty_like(x)
+        ms = time_region(lambda: y.copy_(x), max(steps, 1))
+        return {"config": "copy_1GiB", "ms": ms, "GB/s": 2 * (1 << 30) / (ms * 1e-3) / 1e9}
+    if which == "c2":
+        case, ms, fwd_ms, flops, dkv_ms = bench_varlen_c2(steps, warmup)
+        return {"config": case.name, "ms_per_step": ms, "TFLOP/s": flops / (ms * 1e-3) / 1e12,
+                "fwd_ms": fwd_ms, "dkv_ms": dkv_ms}
+    if which == "c3":
+        case, ms = bench_varlen_c3(max(steps, 1))
+        return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+    case = W.config4(seed=0) if which == "c4" else W.config5(seed=0)
+    ms = bench_absorb(case, max(steps, 1))
+    return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -160,6 +200,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"],
+                    help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the operators have no multi-GPU path "
@@ -169,12 +211,18 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        print(json.dumps(run_only(args.only, args.steps, args.warmup)))
+        return
 
-    case, ms, fwd_ms, flops = bench_varlen_c2(args.steps, args.warmup)
+    case, ms, fwd_ms, flops, dkv_ms = bench_varlen_c2(args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
     fwd_tflops = case.flops_fwd / (fwd_ms * 1e-3) / 1e12
+    # dK/dV kernel: 4 GEMM passes (S recompute, dP, dV, dK) = 8 H D sum(L^2)
+    dkv_flops = 2.0 * case.flops_fwd
+    dkv_tflops = dkv_flops / (dkv_ms * 1e-3) / 1e12
     log(f"C2 fwd+bwd {ms:.3f} ms/step -> {tflops:.1f} TFLOP/s; fwd {fwd_ms:.3f} ms -> "
-        f"{fwd_tflops:.1f} TFLOP/s")
+        f"{fwd_tflops:.1f} TFLOP/s; dK/dV kernel {dkv_ms:.3f} ms -> {dkv_tflops:.1f} TFLOP/s")
     secondary = {}
     if not args.skip_secondary:
         from varlenabsorbflashattn_amd import workloads as W
@@ -210,9 +258,13 @@ def main():
                                "log-uniform[1,4096], q=k lens, non-causal",
                    "seed": 0, "sum_L": int(sum(case.q_lens)),
                    "sum_L2": int(sum(x * x for x in case.q_lens))},
-        "roofline": {"bound": "mfma", "kernel": "varlen_fwd_kernel<bf16,128>",
-                     "achieved": fwd_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": fwd_tflops / BF16_PEAK_TFLOPS, "traffic": None},
+        "roofline": {"bound": "mfma", "kernel": "varlen_dkv_kernel<bf16,128>",
+                     "achieved": dkv_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": dkv_tflops / BF16_PEAK_TFLOPS, "traffic": roofline_traffic(),
+                     "work_per_launch": "8*H*D*sum(L^2) = %.4g FLOP" % dkv_flops,
+                     "ms_per_launch": dkv_ms},
+        "forward_kernel": {"kernel": "varlen_fwd_kernel<bf16,128>", "ms": fwd_ms,
+                           "TFLOP/s": fwd_tflops, "frac": fwd_tflops / BF16_PEAK_TFLOPS},
         "secondary": secondary,
         "cpu_baseline": cpu,
     }

@@ -137,6 +137,23 @@ VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const 
                     int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
                     void *stream);
 
+/* One stage of vafa_varlen_bwd, for callers that schedule the backward
+ * themselves (e.g. dQ and dK/dV on two streams) and for per-kernel timing:
+ *   VAFA_BWD_DELTA (0): delta = rowsum(O * dO) into the workspace;
+ *   VAFA_BWD_DQ    (1): dQ, including the ordered sum of split partials;
+ *   VAFA_BWD_DKV   (2): dK and dV.
+ * Stages 1 and 2 read the delta that stage 0 left in the same workspace and
+ * are independent of each other.  Same arguments as vafa_varlen_bwd. */
+#define VAFA_BWD_DELTA 0
+#define VAFA_BWD_DQ 1
+#define VAFA_BWD_DKV 2
+VAFA_API int vafa_varlen_bwd_stage(int32_t stage, const void *q, const void *k, const void *v,
+                                   const void *o, const void *dout, const float *lse, void *dq,
+                                   void *dk, void *dv, const int32_t *plan_dev,
+                                   const vafa_plan_info *info, int64_t D, int32_t dtype,
+                                   float scale, void *workspace, int64_t workspace_bytes,
+                                   void *stream);
+
 /* Workspace bytes needed by vafa_absorb_fwd / vafa_absorb_bwd. */
 VAFA_API int64_t vafa_absorb_fwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);
 VAFA_API int64_t vafa_absorb_bwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);

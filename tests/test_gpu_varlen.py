@@ -195,3 +195,20 @@ def test_multi_seed(device, seed):
     got, ref = run_case([77, 200, 3], [150, 31, 260], 4, 64, torch.bfloat16, device, seed=seed)
     for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
         assert_close(n, a, r)
+
+
+def test_backward_stages_match_fused(device):
+    """vafa_varlen_bwd_stage (delta, dQ, dK/dV launched separately) reproduces
+    vafa_varlen_bwd bit for bit."""
+    from varlenabsorbflashattn_amd.varlen import BackwardStages
+    q, k, v, cq, ck = _inputs(device, q_lens=(300, 20, 77), k_lens=(9000, 500, 64), D=128)
+    do = torch.randn_like(q)
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o = packed_varlen_attn(qq, kk, vv, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    o.backward(do)
+    st = BackwardStages(q, k, v, do, cq, ck)
+    for s in (0, 1, 2):
+        st.run(s)
+    torch.cuda.synchronize()
+    assert torch.equal(st.o, o.detach())
+    assert torch.equal(st.dq, qq.grad) and torch.equal(st.dk, kk.grad) and torch.equal(st.dv, vv.grad)

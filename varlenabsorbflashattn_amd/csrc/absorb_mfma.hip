@@ -23,10 +23,14 @@ constexpr int kBK = 32;                   // keys per LDS tile
 constexpr int kNBuf = 3;                  // LDS ring depth
 constexpr int kMaxF = 256;                // D_KV handled by this kernel (padded to 32)
 
+#ifndef VAFA_ABS_XPAD
+#define VAFA_ABS_XPAD 8
+#endif
+
 template <int FP>
 struct AbsSmem {
   static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
-  static constexpr int XS = FP + 8;                  // padded row stride (elements)
+  static constexpr int XS = FP + VAFA_ABS_XPAD;      // padded row stride (elements)
   static constexpr int kTile = kBK * XS;             // elements per tile
   static constexpr int kLoopBytes = kNBuf * kTile * 2;
   static constexpr int kEpiBytes = kAbsorbRows * XS * 2;

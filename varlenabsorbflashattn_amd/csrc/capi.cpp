@@ -84,29 +84,41 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
   launch_lse_combine<T>(a.part_o, a.part_lse, a.o, a.lse, a.comb_items, a.n_comb, a.H, a.D, st);
 }
 
-// Matrix-core backward for D in {32, 64, 128}; D=16 and D=256 (whose dK/dV
-// accumulators exceed the register file) take the wave-per-row kernels.
+// Backward stages.  Matrix-core kernels for D in {32, 64, 128}; D=16 and
+// D=256 (whose dK/dV accumulators exceed the register file) take the
+// wave-per-row kernels.
 template <typename T>
-bool varlen_bwd_mfma(const VarlenArgs &a, hipStream_t st) {
-  if constexpr (sizeof(T) == 2) {
-    switch (a.D) {
-      case 32: launch_mfma_varlen_dq<T, 32>(a, st); launch_mfma_varlen_dkv<T, 32>(a, st); return true;
-      case 64: launch_mfma_varlen_dq<T, 64>(a, st); launch_mfma_varlen_dkv<T, 64>(a, st); return true;
-      case 128: launch_mfma_varlen_dq<T, 128>(a, st); launch_mfma_varlen_dkv<T, 128>(a, st); return true;
-      default: break;
+void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
+  const bool mfma = sizeof(T) == 2 && (a.D == 32 || a.D == 64 || a.D == 128);
+  if (stage == VAFA_BWD_DELTA) {
+    launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
+  } else if (stage == VAFA_BWD_DQ) {
+    if constexpr (sizeof(T) == 2) {
+      if (mfma) {
+        if (a.D == 32) launch_mfma_varlen_dq<T, 32>(a, st);
+        if (a.D == 64) launch_mfma_varlen_dq<T, 64>(a, st);
+        if (a.D == 128) launch_mfma_varlen_dq<T, 128>(a, st);
+      }
     }
+    if (!mfma) launch_simt_varlen_dq<T>(a, st);
+    launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, st);
+  } else {
+    if constexpr (sizeof(T) == 2) {
+      if (mfma) {
+        if (a.D == 32) launch_mfma_varlen_dkv<T, 32>(a, st);
+        if (a.D == 64) launch_mfma_varlen_dkv<T, 64>(a, st);
+        if (a.D == 128) launch_mfma_varlen_dkv<T, 128>(a, st);
+      }
+    }
+    if (!mfma) launch_simt_varlen_dkv<T>(a, st);
   }
-  return false;
 }
 
 template <typename T>
 void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
-  launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
-  if (!varlen_bwd_mfma<T>(a, st)) {
-    launch_simt_varlen_dq<T>(a, st);
-    launch_simt_varlen_dkv<T>(a, st);
-  }
-  launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, st);
+  varlen_bwd_stage<T>(VAFA_BWD_DELTA, a, st);
+  varlen_bwd_stage<T>(VAFA_BWD_DQ, a, st);
+  varlen_bwd_stage<T>(VAFA_BWD_DKV, a, st);
 }
 
 // ---- absorb ---------------------------------------------------------------
@@ -174,6 +186,9 @@ int by_dtype(int32_t dtype, const A &a, hipStream_t st) {
 }
 template <typename T> struct VFwd { static void run(const VarlenArgs &a, hipStream_t s) { varlen_fwd_all<T>(a, s); } };
 template <typename T> struct VBwd { static void run(const VarlenArgs &a, hipStream_t s) { varlen_bwd_all<T>(a, s); } };
+template <typename T> struct VBwdStage {
+  static void run(const VarlenArgs &a, hipStream_t s) { varlen_bwd_stage<T>(a.stage, a, s); }
+};
 template <typename T> struct AFwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_fwd_all<T>(a, s); } };
 template <typename T> struct ABwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_bwd_all<T>(a, s); } };
 
@@ -218,14 +233,16 @@ int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float 
   return check_launch("vafa_varlen_fwd");
 }
 
-int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
-                    const void *dout, const float *lse, void *dq, void *dk, void *dv,
-                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
-                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
-                    void *stream) {
+static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const void *v,
+                            const void *o, const void *dout, const float *lse, void *dq, void *dk,
+                            void *dv, const int32_t *plan_dev, const vafa_plan_info *info,
+                            int64_t D, int32_t dtype, float scale, void *workspace,
+                            int64_t workspace_bytes, void *stream) {
   if (int rc = check_info(info, 1)) return rc;
   if (!supported_d(D))
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
+  if (stage < -1 || stage > VAFA_BWD_DKV)
+    return fail(VAFA_ERR_VALUE, "unknown backward stage %d", (int)stage);
   VarlenWs w = carve_varlen(workspace, info, D, true);
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
     return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
@@ -238,8 +255,30 @@ int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
-  if (int rc = by_dtype<VBwd>(dtype, a, (hipStream_t)stream)) return rc;
+  a.stage = stage;
+  const int rc = stage < 0 ? by_dtype<VBwd>(dtype, a, (hipStream_t)stream)
+                           : by_dtype<VBwdStage>(dtype, a, (hipStream_t)stream);
+  if (rc) return rc;
   return check_launch("vafa_varlen_bwd");
+}
+
+int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream) {
+  return varlen_bwd_entry(-1, q, k, v, o, dout, lse, dq, dk, dv, plan_dev, info, D, dtype,
+                          scale, workspace, workspace_bytes, stream);
+}
+
+int vafa_varlen_bwd_stage(int32_t stage, const void *q, const void *k, const void *v,
+                          const void *o, const void *dout, const float *lse, void *dq, void *dk,
+                          void *dv, const int32_t *plan_dev, const vafa_plan_info *info,
+                          int64_t D, int32_t dtype, float scale, void *workspace,
+                          int64_t workspace_bytes, void *stream) {
+  if (stage < 0) return fail(VAFA_ERR_VALUE, "unknown backward stage %d", (int)stage);
+  return varlen_bwd_entry(stage, q, k, v, o, dout, lse, dq, dk, dv, plan_dev, info, D, dtype,
+                          scale, workspace, workspace_bytes, stream);
 }
 
 int64_t vafa_absorb_fwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H) {

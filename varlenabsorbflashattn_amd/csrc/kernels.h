@@ -19,6 +19,7 @@ struct VarlenArgs {
   int64_t T_q;
   int H, D;
   float scale;
+  int stage;  // backward stage (VAFA_BWD_*) or -1 for all
 };
 
 struct AbsorbArgs {

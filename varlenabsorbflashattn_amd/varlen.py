@@ -182,3 +182,53 @@ def packed_varlen_attn(
 
     o3 = _PackedVarlenAttnFunction.apply(q3, k3, v3, cu_seqlens_q, cu_seqlens_k, float(scale))
     return o3.unsqueeze(0) if q_was_4d else o3
+
+
+class BackwardStages:
+    """The three backward stages of packed_varlen_attn as separate launches.
+
+    For profiling and for callers that schedule the backward themselves (the
+    dQ and dK/dV stages are independent once delta is written).  Built from
+    forward inputs; ``run(stage)`` launches one stage on the current stream:
+    0 = delta, 1 = dQ (+ split sums), 2 = dK/dV.
+    """
+
+    def __init__(self, q, k, v, do, cu_seqlens_q, cu_seqlens_k, scale=None):
+        q3, _ = _normalize_qkv(q, "q")
+        k3, _ = _normalize_qkv(k, "k")
+        v3, _ = _normalize_qkv(v, "v")
+        self.D = q3.shape[-1]
+        self.scale = float(scale if scale is not None else 1.0 / math.sqrt(self.D))
+        cu_q_h = _lib.as_host_i64(cu_seqlens_q)
+        cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+        _lib.validate_cu(cu_q_h, q3.shape[0], "cu_seqlens_q")
+        _lib.validate_cu(cu_k_h, k3.shape[0], "cu_seqlens_k")
+        H = q3.shape[1]
+        self.plan = _lib.device_plan("varlen", cu_q_h, cu_k_h, (H, self.D), q3.device)
+        self.q, self.k, self.v = _aligned(q3), _aligned(k3), _aligned(v3)
+        self.do = _aligned(do.reshape(q3.shape).contiguous().to(q3.dtype))
+        # forward through the C ABI (O and the log2-domain LSE)
+        self.lse = torch.empty((q3.shape[0], H), dtype=torch.float32, device=q3.device)
+        L = _lib.lib()
+        fws = _workspace(L.vafa_varlen_fwd_workspace(self.plan.info, self.D), q3.device)
+        o2 = torch.empty_like(self.q)
+        _lib.check(L.vafa_varlen_fwd(
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), o2.data_ptr(),
+            self.lse.data_ptr(), self.plan.items.data_ptr(), self.plan.info, self.D,
+            _lib.dtype_code(q3.dtype), self.scale, fws.data_ptr() if fws.numel() else None,
+            fws.numel(), _lib.stream_ptr(q3.device)))
+        self.o = o2
+        self.dq = torch.empty_like(self.q)
+        self.dk = torch.empty_like(self.k)
+        self.dv = torch.empty_like(self.v)
+        self.ws = _workspace(L.vafa_varlen_bwd_workspace(self.plan.info, self.D), q3.device)
+
+    def run(self, stage: int) -> None:
+        L = _lib.lib()
+        _lib.check(L.vafa_varlen_bwd_stage(
+            int(stage), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+            self.o.data_ptr(), self.do.data_ptr(), self.lse.data_ptr(), self.dq.data_ptr(),
+            self.dk.data_ptr(), self.dv.data_ptr(), self.plan.items.data_ptr(), self.plan.info,
+            self.D, _lib.dtype_code(self.q.dtype), self.scale,
+            self.ws.data_ptr() if self.ws.numel() else None, self.ws.numel(),
+            _lib.stream_ptr(self.q.device)))

@@ -89,17 +89,31 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
   constexpr int NC = D / 16, ND = D / 32;
   constexpr int KS = D + kKPad;
   const int lrow = lane & 31, lhalf = lane >> 5;
+  // S^T for the two 32-key halves as two interleaved MFMA chains; K operands
+  // are read kPre steps ahead so LDS latency hides behind earlier MFMAs.
+  constexpr int kPre = 4;
+  constexpr int NS = 2 * NC;
   f32x16 s[2];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
+  for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+  const T *kbase_p = ks + lrow * KS + lhalf * 8;
+  auto kop = [&](int i) {  // i = cc * 2 + kt
+    return *reinterpret_cast<const u32x4 *>(kbase_p + (i & 1) * 32 * KS + (i >> 1) * 16);
+  };
+  u32x4 ring[kPre];
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      const u32x4 a =
-          *reinterpret_cast<const u32x4 *>(ks + (kt * 32 + lrow) * KS + cc * 16 + lhalf * 8);
-      s[kt] = M::mma(as_v8<T>(a), qf[cc], s[kt]);
-    }
+  for (int i = 0; i < kPre; ++i) ring[i] = kop(i);
+  // sched_barrier(0) pins the written order: the scheduler would otherwise
+  // pull each LDS read down next to its MFMA and expose its latency
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const u32x4 a = ring[i % kPre];
+    s[i & 1] = M::mma(as_v8<T>(a), qf[i >> 1], s[i & 1]);
+    if (i + kPre < NS) ring[i % kPre] = kop(i + kPre);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (kbase + kBN > k_end) {
 #pragma unroll
@@ -139,14 +153,25 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) pb[kt][mm] = pack8<T>(s[kt], mm * 8);
+  // O^T += V^T P^T: 4*ND MFMAs ordered so consecutive ones hit different
+  // accumulators, V^T operands read kPre steps ahead.
+  constexpr int NP = 4 * ND;
+  auto vop = [&](int i) {  // i = km * ND + dt, km = kt * 2 + mm
+    const int km = i / ND, dt = i % ND;
+    return tr_operand<T>(vs, KS, km * 16, dt * 32, lane);
+  };
+  typename M::v8 vring[kPre];
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt)
+  for (int i = 0; i < kPre; ++i) vring[i] = vop(i);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm)
-        acc[dt] = M::mma(tr_operand<T>(vs, KS, kt * 32 + mm * 16, dt * 32, lane), pb[kt][mm],
-                         acc[dt]);
+  for (int i = 0; i < NP; ++i) {
+    const typename M::v8 a = vring[i % kPre];
+    const int km = i / ND, dt = i % ND;
+    acc[dt] = M::mma(a, pb[km >> 1][km & 1], acc[dt]);
+    if (i + kPre < NP) vring[i % kPre] = vop(i + kPre);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 template <typename T, int D>

@@ -128,6 +128,43 @@ def bench_absorb(case, iters):
     return ms
 
 
+def bench_absorb_bwd(case, iters):
+    """Inner absorb forward + backward (grads of u, X, W_V) on precomputed u,
+    validate=False, with a fixed synthetic dO; returns (fwd+bwd ms, fwd ms)."""
+    import torch
+    from varlenabsorbflashattn_amd import prepare_target_attn_indices, target_attn_inner
+    from varlenabsorbflashattn_amd import workloads as W
+    from varlenabsorbflashattn_amd.absorb import _project_u
+    dev = torch.device("cuda:0")
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev)
+    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
+    with torch.no_grad():
+        u = _project_u(q_raw, W_Q, W_K).contiguous()
+    u.requires_grad_(True)
+    X.requires_grad_(True)
+    W_V.requires_grad_(True)
+    scale = 1.0 / math.sqrt(case.D_H)
+    qi, ki = prepare_target_attn_indices(cq, ck)
+    g = torch.Generator().manual_seed(1)
+    dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(dev, torch.bfloat16)
+
+    def step():
+        o = target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
+        o.backward(dO)
+        u.grad = X.grad = W_V.grad = None
+
+    def fwd():
+        with torch.no_grad():
+            target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
+
+    step()
+    ms = time_region(step, iters)
+    f_ms = time_region(fwd, iters)
+    del q_raw, X, u, dO
+    torch.cuda.empty_cache()
+    return ms, f_ms
+
+
 def roofline_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE runs (profiles/roofline_traffic.json), or None."""
@@ -188,6 +225,10 @@ def run_only(which, steps, warmup):
     if which == "c3":
         case, ms = bench_varlen_c3(max(steps, 1))
         return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+    if which == "c4b":
+        case = W.config4(seed=0)
+        ms, f_ms = bench_absorb_bwd(case, max(steps, 1))
+        return {"config": case.name + "_fwd_bwd", "ms": ms, "fwd_ms": f_ms, "bwd_ms": ms - f_ms}
     case = W.config4(seed=0) if which == "c4" else W.config5(seed=0)
     ms = bench_absorb(case, max(steps, 1))
     return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
@@ -200,7 +241,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"],
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4b", "c5", "copy"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,6 +281,10 @@ def main():
                 "TFLOP/s": cfg.flops_fwd / (a_ms * 1e-3) / 1e12,
                 "sum_lq": int(sum(cfg.q_lens)), "sum_lk": int(sum(cfg.k_lens))}
             log(cfg.name, secondary[cfg.name + "_fwd"])
+        c4 = W.config4(seed=0)
+        b_ms, bf_ms = bench_absorb_bwd(c4, max(3, args.steps // 2))
+        secondary[c4.name + "_fwd_bwd"] = {"ms": b_ms, "fwd_ms": bf_ms, "bwd_ms": b_ms - bf_ms}
+        log(c4.name + " fwd+bwd", secondary[c4.name + "_fwd_bwd"])
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     out = {
         "metric": "varlen-FA fwd/bwd TFLOP/s + absorb-attn HBM GB/s, % of MI355X peak",

@@ -99,6 +99,31 @@ def test_absorb_bf16_config4_dims(device):
     assert_close("O", O, O_ref)
 
 
+@pytest.mark.parametrize("seed,n", [(3, 24), (5, 64)])
+def test_absorb_bf16_config4_backward(device, seed, n):
+    """Inner backward at C4 dims (D_in=256, H=8, D_H=32, N(0,1) inputs, Xavier
+    W_V): grads of u, X and W_V against the fp64 oracle."""
+    from varlenabsorbflashattn_amd import workloads as W
+    case = W.config4(seed=seed, n=n)
+    print(f"[absorb c4 bwd] seed={seed} n={n} sum_lq={sum(case.q_lens)} "
+          f"sum_lk={sum(case.k_lens)}", flush=True)
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, "cpu")
+    cq, ck = cu_from_lens(case.q_lens), cu_from_lens(case.k_lens)
+    scale = 1.0 / math.sqrt(case.D_H)
+    u = oa.project_u(*(t.float().numpy() for t in (q_raw, W_Q, W_K)), dtype=np.float64)
+    u_t = torch.from_numpy(u).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(seed + 100)
+    dO = torch.randn(u_t.shape[0], case.H, case.D_H, generator=g).to(torch.bfloat16)
+    dev = [t.to(device).requires_grad_(True) for t in (u_t, X, W_V)]
+    O = target_attn_inner(*dev, cq.to(device), ck.to(device), scale)
+    O.backward(dO.to(device))
+    torch.cuda.synchronize()
+    ref = oa.backward(u_t.float().numpy(), X.float().numpy(), W_V.float().numpy(),
+                      dO.float().numpy(), cq.numpy(), ck.numpy(), scale, np.float64)
+    for name, t, r in zip(("du", "dX", "dW_V"), dev, ref):
+        assert_close(name, t.grad, r)
+
+
 def test_prepared_indices_fast_path(device):
     q_lens, k_lens = [7, 8, 6, 9], [2048, 1024, 1536, 512]
     ins = [t.to(device, torch.bfloat16) for t in make_inputs(q_lens, k_lens)]

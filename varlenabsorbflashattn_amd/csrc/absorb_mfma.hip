@@ -10,47 +10,14 @@
 // operand) and aX^T += X^T P^T (X^T from ds_read_b64_tr_b16), with the online
 // softmax in the log2 domain.  After the key loop aX/l is rounded to the input
 // dtype, regrouped head-major in LDS and projected by W_V (16x16x32 MFMAs).
-#include "kernels.h"
-#include "mfma.h"
+#include "absorb_tiles.h"
 
 namespace vafa {
 
 namespace {
 
-constexpr int kWaves = kAbsorbRows / 32;  // 2 waves x 32 rows
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBK = 32;                   // keys per LDS tile
-constexpr int kNBuf = 3;                  // LDS ring depth
-constexpr int kMaxF = 256;                // D_KV handled by this kernel (padded to 32)
+using namespace absorb;
 
-#ifndef VAFA_ABS_XPAD
-#define VAFA_ABS_XPAD 8
-#endif
-
-template <int FP>
-struct AbsSmem {
-  static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
-  static constexpr int XS = FP + VAFA_ABS_XPAD;      // padded row stride (elements)
-  static constexpr int kTile = kBK * XS;             // elements per tile
-  static constexpr int kLoopBytes = kNBuf * kTile * 2;
-  static constexpr int kEpiBytes = kAbsorbRows * XS * 2;
-  static constexpr int kBytes = kLoopBytes > kEpiBytes ? kLoopBytes : kEpiBytes;
-};
-
-template <typename T>
-struct Mfma16;
-template <>
-struct Mfma16<bf16> {
-  static __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma16<f16> {
-  static __device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
 
 // W_V [F, H, DH] -> wvt [H, DH, FP] (zero-padded over f), the B-operand
 // layout of the projection (8 consecutive f per lane).
@@ -65,27 +32,6 @@ __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__
   const int d = (int)((i / FP) % DH);
   const int h = (int)(i / ((int64_t)FP * DH));
   wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
-}
-
-// Issue the LDS-DMA loads of one 32-key tile: one instruction per X row,
-// lanes 0..CPR-1 each move one 16-byte chunk to the row's padded LDS slot
-// (keys past k_end and chunks past D_KV arrive as zeros).  Every wave issues
-// kBK / kWaves instructions per tile, which keeps vmcnt accounting uniform.
-template <typename T, int FP>
-__device__ __forceinline__ void issue_tile(const T *__restrict__ X, int kb, int k_end, int F,
-                                           T *tile, int wave, int lane) {
-  using S = AbsSmem<FP>;
-  const int rows = k_end - kb < kBK ? (k_end - kb > 0 ? k_end - kb : 0) : kBK;
-  const u32x4 rx = rsrc_words(X + (int64_t)kb * F, (int64_t)rows * F * 2);
-  const int off = lane < F / 8 ? lane * 16 : 0x7fffffff;
-  const uint32_t base = lds_addr(tile);
-  if (lane < S::CPR) {
-#pragma unroll
-    for (int n = 0; n < kBK / kWaves; ++n) {
-      const int r = wave * (kBK / kWaves) + n;
-      lds_dma16(rx, base + r * S::XS * 2, off + r * F * 2);
-    }
-  }
 }
 
 template <typename T, int FP, int DH>
@@ -295,9 +241,10 @@ void launch_dh(const AbsorbArgs &a, const T *wvt, int FP, hipStream_t st) {
   }
 }
 
-inline int padded_f(int F) { return (F + 31) / 32 * 32; }
 
 }  // namespace
+
+using absorb::padded_f;
 
 // The matrix-core path takes H | 64 with at least 8 tokens per workgroup,
 // D_KV a multiple of 8 that pads (to 32) onto one of the compiled widths,

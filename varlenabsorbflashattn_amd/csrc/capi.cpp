@@ -170,8 +170,17 @@ template <typename T>
 void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
   launch_row_dot<T>(a.O_in, a.dO, a.delta, a.T_q * a.H, a.DH, st);
   launch_absorb_dax<T>(a, st);
-  launch_simt_absorb_du<T>(a, st);
-  launch_simt_absorb_dx<T>(a, st);
+  bool mfma = false;
+  if constexpr (sizeof(T) == 2) mfma = mfma_absorb_supported<T>(a.H, a.F, a.DH);
+  if (mfma) {
+    if constexpr (sizeof(T) == 2) {
+      launch_mfma_absorb_du<T>(a, st);
+      launch_mfma_absorb_dx<T>(a, st);
+    }
+  } else {
+    launch_simt_absorb_du<T>(a, st);
+    launch_simt_absorb_dx<T>(a, st);
+  }
   launch_absorb_dwv<T>(a, st);
 }
 

@@ -29,7 +29,8 @@ struct AbsorbArgs {
   const float *lse_in;
   float *delta;
   float *part_o, *part_lse;   // split partial rows [rows, H, D_H] / [rows, H]
-  float *dax, *ax;            // [T_q, H, F] fp32 (backward)
+  void *dax;                  // dO W_V^T [T_q, H, F] in the input dtype (backward)
+  float *ax;                  // aX [T_q, H, F] fp32 (backward, for dW_V)
   float *dwv_part;            // [n_tchunks, F, H, D_H] fp32 (backward)
   void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
   const int32_t *items, *comb_items, *kv_items, *qseg_items;
@@ -77,5 +78,8 @@ template <typename T, int D> void launch_mfma_varlen_dkv(const VarlenArgs &, hip
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
+// absorb_bwd_mfma.hip: du/aX (query side) and dX (key side) on matrix cores
+template <typename T> void launch_mfma_absorb_du(const AbsorbArgs &, hipStream_t);
+template <typename T> void launch_mfma_absorb_dx(const AbsorbArgs &, hipStream_t);
 
 }  // namespace vafa

@@ -11,7 +11,7 @@ constexpr int kVarlenKTile = 128;
 // Absorb: a forward workgroup covers up to kAbsorbRows (token, head) rows;
 // a dX workgroup covers kAbsorbKTile keys.
 constexpr int kAbsorbRows = 64;
-constexpr int kAbsorbKTile = 64;
+constexpr int kAbsorbKTile = 128;
 
 struct SplitPolicy {
   // Query tiles with at most `decode_rows` rows against >= decode_min_keys

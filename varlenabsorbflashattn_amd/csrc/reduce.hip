@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void sum_combine_kernel(const float *__restric
 template <typename T>
 __global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ dO,
                                                          const T *__restrict__ wv,
-                                                         float *__restrict__ dax, int H, int F,
+                                                         T *__restrict__ dax, int H, int F,
                                                          int DH) {
   const int64_t row = blockIdx.x;
   const int h = (int)(row % H);
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ d
     const T *w = wv + ((int64_t)f * H + h) * DH;
     float s = 0.f;
     for (int d = 0; d < DH; ++d) s += sdo[d] * to_f(w[d]);
-    dax[row * F + f] = s;
+    dax[row * F + f] = from_f<T>(s);
   }
 }
 
@@ -165,7 +165,7 @@ template <typename T>
 void launch_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
   if (a.T_q == 0) return;
   hipLaunchKernelGGL(absorb_dax_kernel<T>, dim3((unsigned)(a.T_q * a.H)), dim3(256), 0, st,
-                     (const T *)a.dO, (const T *)a.wv, a.dax, a.H, a.F, a.DH);
+                     (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.H, a.F, a.DH);
 }
 
 template <typename T>

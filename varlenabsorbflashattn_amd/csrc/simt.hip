@@ -264,7 +264,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void simt_absorb_du(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ wv,
     const T *__restrict__ dO, const float *__restrict__ lse, const float *__restrict__ delta,
-    T *__restrict__ du, const float *__restrict__ dax_ws, float *__restrict__ ax_ws,
+    T *__restrict__ du, const T *__restrict__ dax_ws, float *__restrict__ ax_ws,
     const int32_t *__restrict__ cu_items, int H, int F, int DH, float c, float scale) {
   // cu_items: one item per token tile, {t0, t1, k0, k1}: the segment's keys.
   const PlanItem it = load_item(cu_items, blockIdx.x);
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256) void simt_absorb_du(
     for (int i = 0; i < per; ++i) {
       int f = lane + 64 * i;
       uv[i] = f < F ? to_f(u[row * F + f]) : 0.f;
-      dax[i] = f < F ? dax_ws[row * F + f] : 0.f;
+      dax[i] = f < F ? to_f(dax_ws[row * F + f]) : 0.f;
       adu[i] = aax[i] = 0.f;
     }
     const float L = lse[row], dl = delta[row];
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void simt_absorb_du(
 template <typename T>
 __global__ __launch_bounds__(256) void simt_absorb_dx(
     const T *__restrict__ u, const T *__restrict__ X, const float *__restrict__ lse,
-    const float *__restrict__ delta, const float *__restrict__ dax_ws, T *__restrict__ dX,
+    const float *__restrict__ delta, const T *__restrict__ dax_ws, T *__restrict__ dX,
     const int32_t *__restrict__ items, int H, int F, float c, float scale) {
   const PlanItem it = load_item(items, blockIdx.x);
   const int k0 = it.v[0], k1 = it.v[1], t0 = it.v[2], t1 = it.v[3];
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void simt_absorb_dx(
         int f = lane + 64 * i;
         if (f < F) {
           s += xv[i] * to_f(u[row * F + f]);
-          dp += xv[i] * dax_ws[row * F + f];
+          dp += xv[i] * to_f(dax_ws[row * F + f]);
         }
       }
       s = wave_sum(s);
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void simt_absorb_dx(
       const float ds = p * (dp - delta[row]) * scale;
       for (int i = 0; i < per; ++i) {
         int f = lane + 64 * i;
-        if (f < F) acc[i] += ds * to_f(u[row * F + f]) + p * dax_ws[row * F + f];
+        if (f < F) acc[i] += ds * to_f(u[row * F + f]) + p * to_f(dax_ws[row * F + f]);
       }
     }
     for (int i = 0; i < per; ++i) {
@@ -403,7 +403,7 @@ void launch_simt_absorb_du(const AbsorbArgs &a, hipStream_t st) {
   if (a.n_qseg == 0) return;
   hipLaunchKernelGGL(simt_absorb_du<T>, dim3(a.n_qseg), dim3(256), 0, st, (const T *)a.u,
                      (const T *)a.X, (const T *)a.wv, (const T *)a.dO, a.lse_in, a.delta,
-                     (T *)a.du, a.dax, a.ax, a.qseg_items, a.H, a.F, a.DH, a.scale * kLog2e,
+                     (T *)a.du, (const T *)a.dax, a.ax, a.qseg_items, a.H, a.F, a.DH, a.scale * kLog2e,
                      a.scale);
 }
 
@@ -411,7 +411,7 @@ template <typename T>
 void launch_simt_absorb_dx(const AbsorbArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
   hipLaunchKernelGGL(simt_absorb_dx<T>, dim3(a.n_kv), dim3(256), 0, st, (const T *)a.u,
-                     (const T *)a.X, a.lse_in, a.delta, a.dax, (T *)a.dX, a.kv_items, a.H, a.F,
+                     (const T *)a.X, a.lse_in, a.delta, (const T *)a.dax, (T *)a.dX, a.kv_items, a.H, a.F,
                      a.scale * kLog2e, a.scale);
 }
 

@@ -11,8 +11,10 @@
 //       du^T += X^T dS^T, aX^T += X^T P^T   (X^T from ds_read_b64_tr_b16)
 //     du = scale * du is written in the input dtype, aX (for dW_V) in fp32.
 //   * key side, absorb_dx_kernel: one workgroup (4 waves x 32 keys) per key
-//     tile, X held in registers, walking the sample's rows in blocks of 32
-//     staged row-major in LDS by DMA:
+//     chunk, walked in 128-key sub-tiles with X held in registers (the next
+//     sub-tile's rows load while the current one finishes), against the
+//     sample's rows in blocks of 32 staged row-major in LDS by DMA (kept
+//     resident when the sample has at most 64 rows):
 //       S = U X^T, dP = dAX X^T,  dX^T += U^T (scale dS) + dAX^T P
 //     summed over heads in registers (no partial buffers, no atomics).
 // dAX = dO W_V^T arrives in the input dtype: the reference rounds it to that
@@ -25,35 +27,28 @@ namespace {
 
 using namespace absorb;
 
-// LDS-DMA of 32 consecutive rows [F] of a row slab into a padded [32][XS]
-// LDS block (rows past the slab and chunks past F arrive as zeros); each of
-// the workgroup's NW waves moves 32/NW rows, one instruction per row.
+// LDS-DMA of 32 consecutive rows [F] of a row slab (src, bytes) into a
+// padded [32][XS] LDS block (rows past the slab and chunks past F arrive as
+// zeros); each of the workgroup's NW waves moves 32/NW rows, one instruction
+// per row.  The descriptor is rebased per row in scalar registers, so the
+// only per-lane operand is the chunk offset.
 template <int FP, int NW>
-__device__ __forceinline__ void dma_block(const u32x4 &rs, int F, uint32_t base, int wave,
-                                          int lane) {
+__device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
+                                          int wave, int lane) {
   constexpr int XS = AbsSmem<FP>::XS;
   const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
   if (lane < FP / 8) {
 #pragma unroll
     for (int n = 0; n < 32 / NW; ++n) {
       const int r = wave * (32 / NW) + n;
-      lds_dma16(rs, base + r * XS * 2, (int32_t)(off + (uint32_t)(r * F * 2)));
+      const int64_t ro = (int64_t)r * F * 2;
+      lds_dma16(rsrc_words(static_cast<const char *>(src) + ro, bytes - ro), base + r * XS * 2,
+                (int32_t)off);
     }
   }
 }
 
 constexpr int kDuWaves = 4;  // 4 waves x 16 rows = one forward row tile
-
-// A operand of a 16x16x32 product out of a row-major [keys][XS] tile,
-// transposed: lane l gets column f0 + l%16 at the 8 keys of its k slots,
-// slots (l/16)*8 + t <-> keys 4*(l/16) + t (t < 4) and 16 + 4*(l/16) + t - 4.
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::v8 tr_operand16(const T *tile, int stride, int f0,
-                                                             int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const T *p = tile + (4 * g + (i >> 2)) * stride + f0 + 4 * (i & 3);
-  return as_v8<T>(join(lds_tr16(p), lds_tr16(p + 16 * stride)));
-}
 
 template <typename T, int FP>
 __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
@@ -84,7 +79,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
 
   auto issue = [&](int kb, int buf) {
     const int rows = k1 - kb < kBK ? (k1 - kb > 0 ? k1 - kb : 0) : kBK;
-    dma_block<FP, kDuWaves>(rsrc_words(X + (int64_t)kb * F, (int64_t)rows * F * 2), F,
+    dma_block<FP, kDuWaves>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
                             lds_addr(smem + buf * S::kTile), wave, lane);
   };
 #pragma unroll
@@ -120,28 +115,53 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) adu[i][r] = aax[i][r] = 0.f;
 
+  // per-lane element offsets into a tile: X row l16 at f = 8*lq (A operand
+  // of S^T / dP^T) and the origin of the transposed reads (below)
+  const int a_off = l16 * S::XS + lq * 8;
+  const int t_off = (4 * lq + (l16 >> 2)) * S::XS + 4 * (l16 & 3);
+  constexpr int kPre = 4;
+  constexpr int NA = 2 * NK;  // A reads of S^T / dP^T per tile
+  int buf = 0;                // j % kNBuf
   for (int j = 0; j < nt; ++j) {
     wait_vmcnt<(kNBuf - 2) * kPerWave>();
     __syncthreads();
-    issue(k0 + (j + kNBuf - 1) * kBK, (j + kNBuf - 1) % kNBuf);
+    issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
     const int kb = k0 + j * kBK;
-    const T *xs = smem + (j % kNBuf) * S::kTile;
     if (wave_active) {
+      const lds_cptr<T> xa = as_lds(smem + buf * S::kTile + a_off);
+      const lds_cptr<T> xt = as_lds(smem + buf * S::kTile + t_off);
       // S^T, dP^T: two 16-key halves; element r of half mt is key
-      // kb + 16*mt + 4*lq + r of this lane's row
+      // kb + 16*mt + 4*lq + r of this lane's row.  A read i covers half i / NK
+      // and f chunk i % NK; reads run kPre ahead of their products, pinned by
+      // sched_barrier so the scheduler does not sink them next to their use.
+      auto aop = [&](int i) { return lds_ld16<T>(xa + (i / NK) * 16 * S::XS + (i % NK) * 32); };
       f32x4 s[2], dp[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[mt][r] = dp[mt][r] = 0.f;
+      u32x4 ring[kPre];
 #pragma unroll
-        for (int kc = 0; kc < NK; ++kc) {
-          const u32x4 a = *reinterpret_cast<const u32x4 *>(xs + (16 * mt + l16) * S::XS +
-                                                           kc * 32 + lq * 8);
-          s[mt] = M16::mma(as_v8<T>(a), uf[kc], s[mt]);
-          dp[mt] = M16::mma(as_v8<T>(a), gf[kc], dp[mt]);
-        }
+      for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const v8 a = as_v8<T>(ring[i % kPre]);
+        s[i / NK] = M16::mma(a, uf[i % NK], s[i / NK]);
+        dp[i / NK] = M16::mma(a, gf[i % NK], dp[i / NK]);
+        if (i + kPre < NA) ring[i % kPre] = aop(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      // A operand of aX^T / du^T for f tile ft, X^T out of the row-major tile:
+      // lane l gets column 16*ft + l%16 at the keys of its k slots 8*lq + t,
+      // key 4*lq + t (t < 4) and 16 + 4*lq + t - 4 (t >= 4), from two
+      // ds_read_b64_tr_b16.  The first kPre overlap the softmax arithmetic.
+      auto top = [&](int ft) {
+        return as_v8<T>(join(lds_tr8<T>(xt + ft * 16), lds_tr8<T>(xt + 16 * S::XS + ft * 16)));
+      };
+      v8 tring[kPre];
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) tring[i] = top(i);
       const bool tail = kb + kBK > k1;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -152,8 +172,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
           s[mt][r] = p;
           dp[mt][r] = p * (dp[mt][r] - dl);
         }
-      // B operands over the tile's keys: slot 8*lq + t <-> key 4*lq + t (t < 4),
-      // 16 + 4*lq + t - 4 (t >= 4), matching tr_operand16
+      // B operands over the tile's keys in the same slot order
       v8 pb, sb;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -162,13 +181,17 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
         sb[r] = static_cast<T>(dp[0][r]);
         sb[4 + r] = static_cast<T>(dp[1][r]);
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ft = 0; ft < NF; ++ft) {
-        const v8 a = tr_operand16<T>(xs, S::XS, ft * 16, lane);
+        const v8 a = tring[ft % kPre];
         aax[ft] = M16::mma(a, pb, aax[ft]);
         adu[ft] = M16::mma(a, sb, adu[ft]);
+        if (ft + kPre < NF) tring[ft % kPre] = top(ft + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    buf = buf == kNBuf - 1 ? 0 : buf + 1;
   }
   wait_vmcnt<0>();
 
@@ -197,130 +220,364 @@ struct DxSmem {
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
+// Shared pieces of the two dX kernels, for one workgroup's item.
+template <typename T, int FP>
+struct DxItem {
+  using T_ = T;
+  using M = Mfma<T>;
+  using S = DxSmem<FP>;
+  static constexpr int NC = FP / 16;
+  static constexpr int NF = FP / 32;
+  static constexpr int XS = S::XS;
+  static constexpr int kSub = 32 * kDxWaves;  // keys per sub-tile (32 per wave)
+
+  const T *u, *X, *dax;
+  const float *lse, *delta;
+  unsigned char *smem;
+  int k0, k1, r0, r1, F, wave, lane, lrow, lhalf, a_off, t_off;
+
+  __device__ DxItem(const T *u_, const T *X_, const T *dax_, const float *lse_,
+                    const float *delta_, unsigned char *smem_, const PlanItem &it, int H, int F_)
+      : u(u_), X(X_), dax(dax_), lse(lse_), delta(delta_), smem(smem_), F(F_) {
+    k0 = it.v[0];
+    k1 = it.v[1];
+    r0 = it.v[2] * H;
+    r1 = it.v[3] * H;
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    lrow = lane & 31;
+    lhalf = lane >> 5;
+    // row lrow at f = 8*lhalf (A of S and dP) and the origin of the
+    // transposed reads (layout of tr_operand)
+    a_off = lrow * XS + lhalf * 8;
+    t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * XS + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+  }
+  __device__ int nblk() const { return (r1 - r0 + 31) / 32; }
+  __device__ int nsub() const { return (k1 - k0 + kSub - 1) / kSub; }
+
+  // stage 32-row block blk of U, dAX, LSE and delta into buffer buf (rows past
+  // r1 are zero, so they add nothing to dX: both products carry a zero U or
+  // dAX row).  Waves 0/2 move LSE and waves 1/3 delta (the pairs write
+  // identical bytes): one 128-byte DMA per wave keeps vmcnt counts equal.
+  __device__ void issue(int blk, int buf) const {
+    unsigned char *base = smem + buf * S::kBufBytes;
+    const int rb = r0 + blk * 32;
+    const int rows = r1 - rb < 32 ? r1 - rb : 32;
+    const int64_t nb = (int64_t)rows * F * 2;
+    dma_block<FP, kDxWaves>(u + (int64_t)rb * F, nb, F, lds_addr(base), wave, lane);
+    dma_block<FP, kDxWaves>(dax + (int64_t)rb * F, nb, F, lds_addr(base + S::kBlk * 2), wave,
+                            lane);
+    const float *vec = (wave & 1) ? delta : lse;
+    const u32x4 rv = rsrc_words(vec + rb, (int64_t)rows * 4);
+    if (lane < 8) lds_dma16(rv, lds_addr(base + 2 * S::kBlk * 2 + (wave & 1) * 128), lane * 16);
+  }
+
+  // X rows of this wave's 32 keys of sub-tile st: B operand of S = U X^T and
+  // dP = dAX X^T; keys past k1 read as zero.  Waited for at first use.
+  __device__ void load_x(typename M::v8 (&xf)[NC], int st) const {
+    const int kb = k0 + st * kSub;
+    const rsrc_t rx = make_rsrc(X + (int64_t)kb * F, (int64_t)(k1 - kb) * F * 2);
+    const int fchunks = F / 8;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int ch = cc * 2 + lhalf;
+      xf[cc] = as_v8<T>(
+          buf_load16(rx, ch < fchunks ? (wave * 32 + lrow) * F * 2 + ch * 16 : 0x7fffffff));
+    }
+  }
+
+  // P and scale*dS of one staged row block against this wave's keys, packed
+  // as B operands over the block's rows (relabelled C layout: element r of
+  // the S / dP accumulators is row (r/4)*8 + lhalf*4 + r%4, this lane's key)
+  template <int kPre>
+  __device__ void block_p_ds(const typename M::v8 (&xf)[NC], int buf, float c, float scale,
+                             typename M::v8 (&pb)[2], typename M::v8 (&sb)[2]) const {
+    const unsigned char *base = smem + buf * S::kBufBytes;
+    const lds_cptr<T> ub = as_lds(reinterpret_cast<const T *>(base));
+    const lds_cptr<T> gb = ub + S::kBlk;
+    const float *ls = reinterpret_cast<const float *>(base + 2 * S::kBlk * 2);
+    // read i is chunk i/2 of the U (even i) or dAX (odd i) row; reads run
+    // kPre ahead of their products (pinned by sched_barrier)
+    auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? gb : ub) + a_off + (i >> 1) * 16); };
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+    u32x4 ring[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 2 * NC; ++i) {
+      const typename M::v8 a = as_v8<T>(ring[i % kPre]);
+      if (i & 1)
+        dp = M::mma(a, xf[i >> 1], dp);
+      else
+        s = M::mma(a, xf[i >> 1], s);
+      if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 Lv = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
+      const f32x4 Dv = *reinterpret_cast<const f32x4 *>(ls + 32 + g * 8 + lhalf * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = g * 4 + e;
+        const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lv[e]));
+        s[r] = p;
+        dp[r] = p * (dp[r] - Dv[e]) * scale;
+      }
+    }
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      pb[mm] = pack8<T>(s, mm * 8);
+      sb[mm] = pack8<T>(dp, mm * 8);
+    }
+  }
+
+  // transposed A operand of dX^T from a staged block: f tile ft, row half mm,
+  // U (which = 1) or dAX (which = 0)
+  __device__ typename M::v8 top(int buf, int which, int mm, int ft) const {
+    const lds_cptr<T> ub = as_lds(reinterpret_cast<const T *>(smem + buf * S::kBufBytes));
+    const lds_cptr<T> q = (which ? ub : ub + S::kBlk) + t_off + mm * 16 * XS + ft * 32;
+    return as_v8<T>(join(lds_tr8<T>(q), lds_tr8<T>(q + 8 * XS)));
+  }
+
+  // dX[key, f] for f tiles [f0t, f0t + N) of this wave's keys of the sub-tile
+  // at kb, from accumulators with lanes along f: element r of tile i is key
+  // kb + 32*wave + (r/4)*8 + lhalf*4 + r%4 at f = (f0t + i)*32 + lrow
+  template <int N>
+  __device__ void store_rows(T *dX, int kb, int f0t, const f32x16 (&acc)[N]) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int f = (f0t + i) * 32 + lrow;
+      if (f >= F) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + wave * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        if (key < k1) dX[(int64_t)key * F + f] = static_cast<T>(acc[i][r]);
+      }
+    }
+  }
+
+  // dX[key, f] for f tiles [f0t, f0t + n) from this lane's accumulators
+  template <int N>
+  __device__ void store(T *dX, int key, int f0t, const f32x16 (&acc)[N]) const {
+    typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
+    T *dst = dX + (int64_t)key * F;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int f = (f0t + i) * 32 + g * 8 + lhalf * 4;
+        if (f >= F) continue;
+        T4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[i][g * 4 + e]);
+        *reinterpret_cast<T4 *>(dst + f) = w;
+      }
+  }
+};
+
+// dX over NB resident row blocks, in two f halves of (NF+1)/2 tiles each:
+// dX[key, f] += P^T[key, row] dAX[row, f] + (scale dS)^T[key, row] U[row, f]
+// with the packed P / scale*dS as A (their relabelled row order serves as the
+// reduction index) and U / dAX columns from transposed reads as B.  The
+// result has lanes along f, so each store writes 64 contiguous bytes of a
+// key row.
+template <int NB, typename D>
+__device__ __forceinline__ void dx_halves(const D &d, typename D::T_ *dX, int kb,
+                                          const typename D::M::v8 (&pb)[2][2],
+                                          const typename D::M::v8 (&sb)[2][2]) {
+  using v8 = typename D::M::v8;
+  constexpr int NF = D::NF, NH = (NF + 1) / 2, kPre = 4;
+  constexpr int NO = 4 * NB * NH;  // (block, which, mm) x f tiles of a half
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    f32x16 acc[NH];
+#pragma unroll
+    for (int i = 0; i < NH; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    // operand i: f tile h*NH + i % NH (clamped; products past NF are
+    // skipped), block / which / mm from q = i / NH
+    auto op = [&](int i) {
+      const int q = i / NH, ft = h * NH + i % NH;
+      return d.top(q >> 2, q & 1, (q >> 1) & 1, ft < NF ? ft : NF - 1);
+    };
+    v8 tring[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) tring[i] = op(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NO; ++i) {
+      const int q = i / NH, ft = h * NH + i % NH;
+      const v8 a = tring[i % kPre];
+      if (ft < NF) {
+        const v8 aop = (q & 1) ? sb[q >> 2][(q >> 1) & 1] : pb[q >> 2][(q >> 1) & 1];
+        acc[i % NH] = D::M::mma(aop, a, acc[i % NH]);
+      }
+      if (i + kPre < NO) tring[i % kPre] = op(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    d.store_rows(dX, kb, h * NH, acc);
+  }
+}
+
+// Items whose sample has at most 64 rows: both row blocks stay resident for
+// the whole key chunk.  Per 128-key sub-tile each wave forms P and scale*dS
+// for both blocks first (X operands then dead, so the next sub-tile's X loads
+// right away), then accumulates dX^T in two f halves of 64 registers.
+template <typename T, int FP>
+__global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_res_kernel(
+    const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ dax,
+    const float *__restrict__ lse, const float *__restrict__ delta, T *__restrict__ dX,
+    const int32_t *__restrict__ items, int H, int F, float c, float scale) {
+  using D = DxItem<T, FP>;
+  using v8 = typename D::M::v8;
+  constexpr int kPre = 4;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const D d(u, X, dax, lse, delta, smem_raw, load_item(items, blockIdx.x), H, F);
+  const int nblk = d.nblk();
+  if (nblk > 2) return;  // streamed by absorb_dx_kernel
+  const int nsub = d.nsub();
+  if (nblk == 0) {
+    // a sample without queries: its keys get zero gradient
+    f32x16 zero[D::NF];
+#pragma unroll
+    for (int i = 0; i < D::NF; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) zero[i][r] = 0.f;
+    for (int st = 0; st < nsub; ++st) {
+      const int key = d.k0 + st * D::kSub + d.wave * 32 + d.lrow;
+      if (key < d.k1) d.store(dX, key, 0, zero);
+    }
+    return;
+  }
+  for (int b = 0; b < nblk; ++b) d.issue(b, b);
+  v8 xf[D::NC];
+  d.load_x(xf, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  for (int st = 0; st < nsub; ++st) {
+    const int kb = d.k0 + st * D::kSub;
+    if (kb + d.wave * 32 >= d.k1) break;  // wave-uniform: no keys left for this wave
+    const int key = kb + d.wave * 32 + d.lrow;
+    v8 pb[2][2], sb[2][2];
+    d.template block_p_ds<kPre>(xf, 0, c, scale, pb[0], sb[0]);
+    if (nblk > 1) d.template block_p_ds<kPre>(xf, 1, c, scale, pb[1], sb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (st + 1 < nsub) d.load_x(xf, st + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nblk > 1)
+      dx_halves<2>(d, dX, kb, pb, sb);
+    else
+      dx_halves<1>(d, dX, kb, pb, sb);
+  }
+  wait_vmcnt<0>();
+}
+
+// Items whose sample has more than 64 rows: per 128-key sub-tile the row
+// blocks stream through two buffers and dX^T accumulates over all of them.
 template <typename T, int FP>
 __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ dax,
     const float *__restrict__ lse, const float *__restrict__ delta, T *__restrict__ dX,
     const int32_t *__restrict__ items, int H, int F, float c, float scale) {
-  using M = Mfma<T>;
-  using S = DxSmem<FP>;
-  constexpr int NC = FP / 16;
-  constexpr int NF = FP / 32;
-  constexpr int XS = S::XS;
+  using D = DxItem<T, FP>;
+  using v8 = typename D::M::v8;
+  constexpr int NF = D::NF;
+  constexpr int kPre = FP >= 224 ? 1 : 4;  // operand prefetch depth within the register budget
   extern __shared__ __align__(16) unsigned char smem_raw[];
-
-  const PlanItem it = load_item(items, blockIdx.x);
-  const int k0 = it.v[0], k1 = it.v[1], t0 = it.v[2], t1 = it.v[3];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  const int key = k0 + wave * 32 + lrow;
-  const bool key_ok = key < k1;
-  const bool wave_active = k0 + wave * 32 < k1;
-  const int r0 = t0 * H, r1 = t1 * H;
-  const int nblk = (r1 - r0 + 31) / 32;
-
-  // stage one 32-row block of U, dAX, LSE and delta (rows past r1 are zero,
-  // so they add nothing to dX: both products carry a zero U or dAX row)
-  auto issue = [&](int blk, int buf) {
-    unsigned char *base = smem_raw + buf * S::kBufBytes;
-    const int rb = r0 + blk * 32;
-    const int rows = r1 - rb < 32 ? r1 - rb : 32;
-    const int64_t nb = (int64_t)rows * F * 2;
-    dma_block<FP, kDxWaves>(rsrc_words(u + (int64_t)rb * F, nb), F, lds_addr(base), wave, lane);
-    dma_block<FP, kDxWaves>(rsrc_words(dax + (int64_t)rb * F, nb), F,
-                            lds_addr(base + S::kBlk * 2), wave, lane);
-    // waves 0/2 move LSE and waves 1/3 delta (the pairs write identical bytes):
-    // one 128-byte DMA per wave keeps every wave's vmcnt count equal
-    const float *vec = (wave & 1) ? delta : lse;
-    const u32x4 rv = rsrc_words(vec + rb, (int64_t)rows * 4);
-    if (lane < 8)
-      lds_dma16(rv, lds_addr(base + 2 * S::kBlk * 2 + (wave & 1) * 128), lane * 16);
-  };
-
-  if (nblk > 0) issue(0, 0);
-
-  // X rows of this wave's 32 keys: B operand of S = U X^T and dP = dAX X^T
-  typename M::v8 xf[NC];
-  {
-    const rsrc_t rx = make_rsrc(X + (int64_t)k0 * F, (int64_t)(k1 - k0) * F * 2);
-    const int fchunks = F / 8;
+  const D d(u, X, dax, lse, delta, smem_raw, load_item(items, blockIdx.x), H, F);
+  const int nblk = d.nblk();
+  if (nblk <= 2) return;  // resident items: absorb_dx_res_kernel
+  const int nsub = d.nsub();
+  v8 xf[D::NC];
+  d.issue(0, 0);
+  int jb = 0;  // streamed blocks consumed so far (buffer parity)
+  for (int st = 0; st < nsub; ++st) {
+    const int kb = d.k0 + st * D::kSub;
+    const int key = kb + d.wave * 32 + d.lrow;
+    const bool wave_active = kb + d.wave * 32 < d.k1;
+    d.load_x(xf, st);
+    f32x16 acc[NF];
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      const int ch = cc * 2 + lhalf;
-      u32x4 w = buf_load16(rx, ch < fchunks ? (wave * 32 + lrow) * F * 2 + ch * 16 : 0x7fffffff);
-      asm volatile("" : "+v"(w));
-      xf[cc] = as_v8<T>(w);
+    for (int i = 0; i < NF; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    for (int j = 0; j < nblk; ++j) {
+      wait_vmcnt<0>();
+      __syncthreads();  // block visible; every wave is done with the other buffer
+      const int buf = jb & 1;
+      // next streamed block: this sub-tile's j+1, or block 0 of the next one
+      if (j + 1 < nblk)
+        d.issue(j + 1, buf ^ 1);
+      else if (st + 1 < nsub)
+        d.issue(0, buf ^ 1);
+      ++jb;
+      if (!wave_active) continue;
+      v8 pb[2], sb[2];
+      d.template block_p_ds<kPre>(xf, buf, c, scale, pb, sb);
+      v8 tring[kPre];
+      auto op = [&](int i) { return d.top(buf, (i / NF) & 1, (i / NF) >> 1, i % NF); };
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) tring[i] = op(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4 * NF; ++i) {
+        const int ft = i % NF, mm = (i / NF) >> 1;
+        const v8 a = tring[i % kPre];
+        acc[ft] = D::M::mma(a, ((i / NF) & 1) ? sb[mm] : pb[mm], acc[ft]);
+        if (i + kPre < 4 * NF) tring[i % kPre] = op(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (wave_active && key < d.k1) d.store(dX, key, 0, acc);
+  }
+  wait_vmcnt<0>();
+}
+
+// dAX[t,h,f] = sum_d dO[t,h,d] W_V[f,h,d] (ta/kernels.py:474-476), rounded to
+// the input dtype.  One wave per (32 tokens, head): dAX = dO W_V^T with dO rows
+// as A (32 tokens x 16 d) and W_V rows as B (16 d x 32 f), f tiles in turn.
+template <typename T, int DH>
+__global__ __launch_bounds__(64) void absorb_dax_kernel(const T *__restrict__ dO,
+                                                        const T *__restrict__ wv,
+                                                        T *__restrict__ dax, int64_t T_q, int H,
+                                                        int F) {
+  using M = Mfma<T>;
+  constexpr int KC = DH / 16;
+  const int lane = threadIdx.x, l32 = lane & 31, lh = lane >> 5;
+  const int h = (int)(blockIdx.x % H);
+  const int64_t t0 = (int64_t)(blockIdx.x / H) * 32;
+  const int nt = T_q - t0 < 32 ? (int)(T_q - t0) : 32;
+  // tokens past T_q and W_V rows past F read as zero
+  const rsrc_t rd = make_rsrc(dO + t0 * H * DH, (int64_t)nt * H * DH * 2);
+  const rsrc_t rw = make_rsrc(wv, (int64_t)F * H * DH * 2);
+  typename M::v8 a[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+    a[kc] = as_v8<T>(buf_load16(rd, ((l32 * H + h) * DH + kc * 16 + lh * 8) * 2));
+  const int nft = (F + 31) / 32;
+  for (int ft = 0; ft < nft; ++ft) {
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const u32x4 b = buf_load16(rw, (((ft * 32 + l32) * H + h) * DH + kc * 16 + lh * 8) * 2);
+      acc = M::mma(a[kc], as_v8<T>(b), acc);
+    }
+    // element r: token (r/4)*8 + lh*4 + r%4, f = ft*32 + l32
+    const int f = ft * 32 + l32;
+    if (f >= F) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int tk = (r >> 2) * 8 + lh * 4 + (r & 3);
+      if (tk < nt) dax[((t0 + tk) * H + h) * F + f] = static_cast<T>(acc[r]);
     }
   }
-  f32x16 acc[NF];
-#pragma unroll
-  for (int i = 0; i < NF; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  for (int j = 0; j < nblk; ++j) {
-    wait_vmcnt<0>();
-    __syncthreads();  // block j visible; every wave is done with block j-1's buffer
-    if (j + 1 < nblk) issue(j + 1, (j + 1) & 1);
-    if (wave_active) {
-      const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
-      const T *us = reinterpret_cast<const T *>(base);
-      const T *gs = us + S::kBlk;
-      const float *ls = reinterpret_cast<const float *>(base + 2 * S::kBlk * 2);
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(us + lrow * XS + cc * 16 + lhalf * 8);
-        s = M::mma(as_v8<T>(a), xf[cc], s);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(gs + lrow * XS + cc * 16 + lhalf * 8);
-        dp = M::mma(as_v8<T>(b), xf[cc], dp);
-      }
-      // element r holds row (r/4)*8 + lhalf*4 + r%4 of the block, this lane's key
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 Lv = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
-        const f32x4 Dv = *reinterpret_cast<const f32x4 *>(ls + 32 + g * 8 + lhalf * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = g * 4 + e;
-          const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lv[e]));
-          s[r] = p;
-          dp[r] = p * (dp[r] - Dv[e]) * scale;
-        }
-      }
-      typename M::v8 pb[2], sb[2];
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        pb[mm] = pack8<T>(s, mm * 8);
-        sb[mm] = pack8<T>(dp, mm * 8);
-      }
-#pragma unroll
-      for (int ft = 0; ft < NF; ++ft)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          acc[ft] = M::mma(tr_operand<T>(gs, XS, mm * 16, ft * 32, lane), pb[mm], acc[ft]);
-          acc[ft] = M::mma(tr_operand<T>(us, XS, mm * 16, ft * 32, lane), sb[mm], acc[ft]);
-        }
-    }
-  }
-
-  if (!key_ok) return;
-  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-  T *dst = dX + (int64_t)key * F;
-#pragma unroll
-  for (int ft = 0; ft < NF; ++ft)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int f = ft * 32 + g * 8 + lhalf * 4;
-      if (f >= F) continue;
-      T4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[ft][g * 4 + e]);
-      *reinterpret_cast<T4 *>(dst + f) = w;
-    }
 }
 
 template <typename T, int FP>
@@ -336,6 +593,12 @@ void launch_du_fp(const AbsorbArgs &a, hipStream_t st) {
 template <typename T, int FP>
 void launch_dx_fp(const AbsorbArgs &a, hipStream_t st) {
   const int smem = DxSmem<FP>::kBytes;
+  // both kernels walk the whole key-chunk section; each skips the other's items
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_res_kernel<T, FP>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  hipLaunchKernelGGL((absorb_dx_res_kernel<T, FP>), dim3((unsigned)a.n_kv), dim3(64 * kDxWaves),
+                     smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
+                     a.delta, (T *)a.dX, a.kv_items, a.H, a.F, a.scale * kLog2e, a.scale);
   hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)a.n_kv), dim3(64 * kDxWaves),
@@ -371,6 +634,21 @@ void launch_mfma_absorb_dx(const AbsorbArgs &a, hipStream_t st) {
   }
 }
 
+template <typename T>
+bool launch_mfma_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
+  if (a.T_q == 0) return true;
+  const unsigned grid = (unsigned)(((a.T_q + 31) / 32) * a.H);
+  switch (a.DH) {
+    case 16: hipLaunchKernelGGL((absorb_dax_kernel<T, 16>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
+    case 32: hipLaunchKernelGGL((absorb_dax_kernel<T, 32>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
+    case 64: hipLaunchKernelGGL((absorb_dax_kernel<T, 64>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
+    case 128: hipLaunchKernelGGL((absorb_dax_kernel<T, 128>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
+    default: return false;
+  }
+}
+
+template bool launch_mfma_absorb_dax<bf16>(const AbsorbArgs &, hipStream_t);
+template bool launch_mfma_absorb_dax<f16>(const AbsorbArgs &, hipStream_t);
 template void launch_mfma_absorb_du<bf16>(const AbsorbArgs &, hipStream_t);
 template void launch_mfma_absorb_du<f16>(const AbsorbArgs &, hipStream_t);
 template void launch_mfma_absorb_dx<bf16>(const AbsorbArgs &, hipStream_t);

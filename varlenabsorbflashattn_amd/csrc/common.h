@@ -115,18 +115,18 @@ struct alignas(16) PlanItem {
   int32_t v[8];
 };
 
+// Every lane of a workgroup reads the same item; readfirstlane makes that
+// visible to the compiler, so item-derived ranges, addresses and buffer
+// descriptors live in scalar registers and steer scalar branches.
 __device__ __forceinline__ PlanItem load_item(const int32_t *plan, int64_t idx) {
   const u32x4 *p = reinterpret_cast<const u32x4 *>(plan + idx * 8);
   u32x4 a = p[0], b = p[1];
   PlanItem it;
-  it.v[0] = (int32_t)a[0];
-  it.v[1] = (int32_t)a[1];
-  it.v[2] = (int32_t)a[2];
-  it.v[3] = (int32_t)a[3];
-  it.v[4] = (int32_t)b[0];
-  it.v[5] = (int32_t)b[1];
-  it.v[6] = (int32_t)b[2];
-  it.v[7] = (int32_t)b[3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    it.v[i] = __builtin_amdgcn_readfirstlane((int32_t)a[i]);
+    it.v[4 + i] = __builtin_amdgcn_readfirstlane((int32_t)b[i]);
+  }
   return it;
 }
 

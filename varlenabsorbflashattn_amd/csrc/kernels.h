@@ -80,6 +80,8 @@ int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
 // absorb_bwd_mfma.hip: du/aX (query side) and dX (key side) on matrix cores
 template <typename T> void launch_mfma_absorb_du(const AbsorbArgs &, hipStream_t);
+// dAX = dO W_V^T; false (nothing launched) for a D_H it does not cover
+template <typename T> bool launch_mfma_absorb_dax(const AbsorbArgs &, hipStream_t);
 template <typename T> void launch_mfma_absorb_dx(const AbsorbArgs &, hipStream_t);
 
 }  // namespace vafa

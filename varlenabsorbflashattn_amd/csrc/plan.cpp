@@ -364,7 +364,7 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
     for (int64_t k = k0; k < k1; k += BK) {
       const int64_t ke = std::min(k + BK, k1);
       Item it{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s, 0, 0, 0},
-              (lq * H + pol.item_overhead)};
+              (round_up(ke - k, 128) * round_up(lq * H, 32) + pol.item_overhead)};
       kv.push_back(it);
     }
   }

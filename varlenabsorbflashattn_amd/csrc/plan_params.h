@@ -9,9 +9,10 @@ namespace vafa {
 constexpr int kVarlenQTile = 128;
 constexpr int kVarlenKTile = 128;
 // Absorb: a forward workgroup covers up to kAbsorbRows (token, head) rows;
-// a dX workgroup covers kAbsorbKTile keys.
+// a dX workgroup covers up to kAbsorbKTile keys of one sample (four 128-key
+// sub-tiles on the matrix-core path).
 constexpr int kAbsorbRows = 64;
-constexpr int kAbsorbKTile = 128;
+constexpr int kAbsorbKTile = 512;
 
 struct SplitPolicy {
   // Query tiles with at most `decode_rows` rows against >= decode_min_keys

@@ -102,23 +102,53 @@ __global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ d
   }
 }
 
-// dW_V partial over one token chunk: part[c, f, h, d] = sum_{t in chunk} aX[t,h,f] dO[t,h,d]
+// dW_V partial over one token chunk, part[c, f, h, d] = sum_{t in chunk}
+// aX[t,h,f] dO[t,h,d], on fp32 matrix cores (v_mfma_f32_32x32x2f32, aX kept in
+// fp32).  One wave per (chunk, head, 32-wide f slice, 32-wide d tile):
+// dW_V^T[d, f] += dO^T[d, t] aX[t, f] two tokens per product, lane l feeding
+// token t + l/32 at d (A) and f (B) = l % 32.
 template <typename T>
-__global__ __launch_bounds__(256) void absorb_dwv_part_kernel(
+__global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
     const float *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
     int64_t T_q, int64_t tchunk, int H, int F, int DH) {
-  const int64_t n_out = (int64_t)F * H * DH;
-  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (o >= n_out) return;
-  const int d = (int)(o % DH);
-  const int h = (int)((o / DH) % H);
-  const int f = (int)(o / ((int64_t)DH * H));
-  const int64_t c = blockIdx.y;
-  const int64_t t0 = c * tchunk, t1 = t0 + tchunk < T_q ? t0 + tchunk : T_q;
-  float s = 0.f;
-  for (int64_t t = t0; t < t1; ++t)
-    s += ax[(t * H + h) * F + f] * to_f(dO[(t * H + h) * DH + d]);
-  part[c * n_out + o] = s;
+  const int lane = threadIdx.x, l32 = lane & 31, kt = lane >> 5;
+  const int nfs = (F + 31) / 32, nds = (DH + 31) / 32;
+  int w = blockIdx.x;
+  const int ds = w % nds;
+  w /= nds;
+  const int fs = w % nfs;
+  w /= nfs;
+  const int h = w % H;
+  const int64_t c = w / H;
+  const int64_t ta = c * tchunk, tb = ta + tchunk < T_q ? ta + tchunk : T_q;
+  const int f = fs * 32 + l32, d = ds * 32 + l32;
+  const bool f_ok = f < F, d_ok = d < DH;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  constexpr int kU = 8;  // token pairs per batch of loads
+  for (int64_t t = ta; t < tb; t += 2 * kU) {
+    float av[kU], bv[kU];
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      const int64_t tt = t + 2 * i + kt;
+      const bool ok = tt < tb;
+      av[i] = ok && d_ok ? to_f(dO[(tt * H + h) * DH + d]) : 0.f;
+      bv[i] = ok && f_ok ? ax[(tt * H + h) * F + f] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kU; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[i], acc, 0, 0, 0);
+  }
+  // acc element r: d = ds*32 + (r/4)*8 + kt*4 + r%4, f = this lane's f
+  if (!f_ok) return;
+  float *dst = part + ((c * F + f) * H + h) * DH;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int d0 = ds * 32 + g * 8 + kt * 4;
+    if (d0 >= DH) continue;
+    f32x4 v = {acc[g * 4], acc[g * 4 + 1], acc[g * 4 + 2], acc[g * 4 + 3]};
+    *reinterpret_cast<f32x4 *>(dst + d0) = v;
+  }
 }
 
 template <typename T>
@@ -172,9 +202,9 @@ template <typename T>
 void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
   const int64_t n_out = (int64_t)a.F * a.H * a.DH;
   if (a.n_tchunks > 0) {
-    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3(blocks_for(n_out), (unsigned)a.n_tchunks),
-                       dim3(256), 0, st, a.ax, (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H,
-                       a.F, a.DH);
+    const int64_t waves = a.n_tchunks * a.H * ((a.F + 31) / 32) * ((a.DH + 31) / 32);
+    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3((unsigned)waves), dim3(64), 0, st, a.ax,
+                       (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH);
   }
   hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st,
                      a.dwv_part, (T *)a.dwv, n_out, a.n_tchunks);

@@ -346,16 +346,24 @@ struct DxItem {
   // dX[key, f] for f tiles [f0t, f0t + N) of this wave's keys of the sub-tile
   // at kb, from accumulators with lanes along f: element r of tile i is key
   // kb + 32*wave + (r/4)*8 + lhalf*4 + r%4 at f = (f0t + i)*32 + lrow
+  // Buffer stores: keys past k1 fall outside the descriptor and are dropped.
+  // Each offset is one add of a scalar row term, written as volatile asm so
+  // the compiler does not hoist all 16*N offsets into registers.
   template <int N>
   __device__ void store_rows(T *dX, int kb, int f0t, const f32x16 (&acc)[N]) const {
+    const rsrc_t rs = make_rsrc(dX + (int64_t)kb * F, (int64_t)(k1 - kb) * F * 2);
+    const int lane_off = ((wave * 32 + lhalf * 4) * F + lrow) * 2;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int f = (f0t + i) * 32 + lrow;
       if (f >= F) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kb + wave * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-        if (key < k1) dX[(int64_t)key * F + f] = static_cast<T>(acc[i][r]);
+        const int row_term = (((r >> 2) * 8 + (r & 3)) * F + (f0t + i) * 32) * 2;
+        int off;
+        asm volatile("v_add_u32 %0, %1, %2" : "=v"(off) : "s"(row_term), "v"(lane_off));
+        __builtin_amdgcn_raw_buffer_store_b16(
+            __builtin_bit_cast(unsigned short, static_cast<T>(acc[i][r])), rs, off, 0, 0);
       }
     }
   }

@@ -27,27 +27,6 @@ namespace {
 
 using namespace absorb;
 
-// LDS-DMA of 32 consecutive rows [F] of a row slab (src, bytes) into a
-// padded [32][XS] LDS block (rows past the slab and chunks past F arrive as
-// zeros); each of the workgroup's NW waves moves 32/NW rows, one instruction
-// per row.  The descriptor is rebased per row in scalar registers, so the
-// only per-lane operand is the chunk offset.
-template <int FP, int NW>
-__device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
-                                          int wave, int lane) {
-  constexpr int XS = AbsSmem<FP>::XS;
-  const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
-  if (lane < FP / 8) {
-#pragma unroll
-    for (int n = 0; n < 32 / NW; ++n) {
-      const int r = wave * (32 / NW) + n;
-      const int64_t ro = (int64_t)r * F * 2;
-      lds_dma16(rsrc_words(static_cast<const char *>(src) + ro, bytes - ro), base + r * XS * 2,
-                (int32_t)off);
-    }
-  }
-}
-
 constexpr int kDuWaves = 4;  // 4 waves x 16 rows = one forward row tile
 
 template <typename T, int FP>

@@ -1,15 +1,17 @@
 // Absorbed ragged target attention forward on gfx950 matrix cores
 // (replaces ta/kernels.py:185-284, the default "alpha" forward).
 //
-// One workgroup = 2 waves owns up to 64 (token, head) rows of one sample --
-// all H heads of 64/H consecutive tokens, token-major, so the rows are one
-// contiguous slab of u -- and one key range.  Raw X is streamed once per
-// workgroup (not once per head) through a 3-deep ring of 32-key LDS tiles
+// One workgroup = 4 waves x 16 rows owns up to 64 (token, head) rows of one
+// sample -- all H heads of 64/H consecutive tokens, token-major, so the rows
+// are one contiguous slab of u -- and one key range.  Raw X is streamed once
+// per workgroup (not once per head) through a 3-deep ring of 32-key LDS tiles
 // filled by buffer_load ... lds, one instruction per padded row (no staging
-// registers; rows past the key range arrive as zeros).  Per tile each wave issues S^T = X U^T (X rows as the A
-// operand) and aX^T += X^T P^T (X^T from ds_read_b64_tr_b16), with the online
-// softmax in the log2 domain.  After the key loop aX/l is rounded to the input
-// dtype, regrouped head-major in LDS and projected by W_V (16x16x32 MFMAs).
+// registers; rows past the key range arrive as zeros).  Per tile each wave
+// issues S^T = X U^T (X rows as the A operand) and aX^T += X^T P^T (X^T from
+// ds_read_b64_tr_b16) as 16x16x32 products, LDS operands read a few products
+// ahead, with the online softmax in the log2 domain.  After the key loop aX/l
+// is rounded to the input dtype, regrouped head-major in LDS and projected by
+// W_V (16x16x32 products).
 #include "absorb_tiles.h"
 
 namespace vafa {
@@ -34,16 +36,20 @@ __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__
   wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
 }
 
+constexpr int kFwdWaves = 4;  // 4 waves x 16 rows = kAbsorbRows
+
 template <typename T, int FP, int DH>
-__global__ __launch_bounds__(kThreads, 2) void absorb_fwd_kernel(
+__global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ wvt,
     T *__restrict__ O, float *__restrict__ lse, float *__restrict__ part_o,
     float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, int F, float c) {
-  using M = Mfma<T>;
+  using M16 = Mfma16<T>;
+  using v8 = typename Mfma<T>::v8;
   using S = AbsSmem<FP>;
-  constexpr int NC = FP / 16;   // S^T reduction chunks
-  constexpr int NF = FP / 32;   // aX^T row tiles
-  constexpr int kPerWave = kBK / kWaves;  // DMA instructions per wave per tile
+  constexpr int NK = FP / 32;   // 32-wide reduction chunks of S^T
+  constexpr int NF = FP / 16;   // 16-row f tiles of aX^T
+  constexpr int kPerWave = kBK / kFwdWaves;  // DMA instructions per wave per tile
+  constexpr int kPre = 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
@@ -51,82 +57,101 @@ __global__ __launch_bounds__(kThreads, 2) void absorb_fwd_kernel(
   const int t0 = it.v[0], t1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
   if (t1 <= t0) return;  // no-op slot of the XCD-aware layout
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
   const int nrows = (t1 - t0) * H;
-  const int row = wave * 32 + lrow;  // local (token-major) row
+  const int row = wave * 16 + l16;  // local (token-major) row
   const bool row_ok = row < nrows;
-  const bool wave_active = wave * 32 < nrows;
+  const bool wave_active = wave * 16 < nrows;
   const int nt = (k1 - k0 + kBK - 1) / kBK;
 
-  // start the first kNBuf-1 tiles before anything else
+  auto issue = [&](int kb, int buf) {
+    const int rows = k1 - kb < kBK ? (k1 - kb > 0 ? k1 - kb : 0) : kBK;
+    dma_block<FP, kFwdWaves>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
+                             lds_addr(smem + buf * S::kTile), wave, lane);
+  };
 #pragma unroll
-  for (int b = 0; b < kNBuf - 1; ++b)
-    issue_tile<T, FP>(X, k0 + b * kBK, k1, F, smem + b * S::kTile, wave, lane);
+  for (int b = 0; b < kNBuf - 1; ++b) issue(k0 + b * kBK, b);
 
-  // U^T fragments (B operand of S^T = X U^T)
-  typename M::v8 uf[NC];
+  // U^T fragments (B operand of S^T = X U^T): row `row`, f = 32*kc + 8*lq + t
+  v8 uf[NK];
   {
     const rsrc_t ru = make_rsrc(u + (int64_t)t0 * H * F, (int64_t)nrows * F * 2);
     const int fchunks = F / 8;
+    // a negative scale is folded into u (sign flip of every element)
+    const uint32_t usign = c < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      const int ch = cc * 2 + lhalf;
+    for (int kc = 0; kc < NK; ++kc) {
+      const int ch = kc * 4 + lq;
       u32x4 w = buf_load16(ru, ch < fchunks ? row * F * 2 + ch * 16 : 0x7fffffff);
-      // pass through an empty asm: the compiler waits for the load here, in
-      // the prologue, instead of before every use inside the key loop (where
-      // its vmcnt waits would also drain the LDS-DMA prefetch)
+      // waited for here, in the prologue, not inside the key loop where a
+      // compiler vmcnt wait would also drain the LDS-DMA ring
       asm volatile("" : "+v"(w));
-      uf[cc] = as_v8<T>(w);
-    }
-  }
-  f32x16 acc[NF];
-#pragma unroll
-  for (int i = 0; i < NF; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-  float m_run = kNegInf, l_part = 0.f;
-  const uint32_t usign = c < 0.f ? 0x80008000u : 0u;  // fold a negative scale into u
-  if (usign) {
-#pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      u32x4 w = __builtin_bit_cast(u32x4, uf[cc]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) w[e] ^= usign;
-      uf[cc] = as_v8<T>(w);
+      uf[kc] = as_v8<T>(w);
     }
   }
   c = fabsf(c);
+  f32x4 acc[NF];
+#pragma unroll
+  for (int i = 0; i < NF; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
+  float m_run = kNegInf, l_part = 0.f;
 
+  const int a_off = l16 * S::XS + lq * 8;
+  const int t_off = (4 * lq + (l16 >> 2)) * S::XS + 4 * (l16 & 3);
+  int buf = 0;  // j % kNBuf
   for (int j = 0; j < nt; ++j) {
     // tile j landed (later tiles may still be in flight), visible to all waves,
     // and every wave is done with tile j-1 whose slot is refilled next
     wait_vmcnt<(kNBuf - 2) * kPerWave>();
     __syncthreads();
-    issue_tile<T, FP>(X, k0 + (j + kNBuf - 1) * kBK, k1, F,
-                      smem + ((j + kNBuf - 1) % kNBuf) * S::kTile, wave, lane);
+    issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
     const int kb = k0 + j * kBK;
-    const T *xs = smem + (j % kNBuf) * S::kTile;
     if (wave_active) {
-      f32x16 s;
+      const lds_cptr<T> xa = as_lds(smem + buf * S::kTile + a_off);
+      const lds_cptr<T> xt = as_lds(smem + buf * S::kTile + t_off);
+      // S^T in two 16-key halves: element r of half mt is key
+      // kb + 16*mt + 4*lq + r of this lane's row; A reads run kPre ahead
+      auto aop = [&](int i) { return lds_ld16<T>(xa + (i / NK) * 16 * S::XS + (i % NK) * 32); };
+      f32x4 s[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a =
-            *reinterpret_cast<const u32x4 *>(xs + lrow * S::XS + cc * 16 + lhalf * 8);
-        s = M::mma(as_v8<T>(a), uf[cc], s);
+        for (int r = 0; r < 4; ++r) s[mt][r] = 0.f;
+      u32x4 ring[kPre];
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 2 * NK; ++i) {
+        s[i / NK] = M16::mma(as_v8<T>(ring[i % kPre]), uf[i % NK], s[i / NK]);
+        if (i + kPre < 2 * NK) ring[i % kPre] = aop(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      // X^T operands of aX^T: lane l gets column 16*ft + l%16 at the keys of
+      // its k slots 8*lq + t <-> key 4*lq + t (t < 4), 16 + 4*lq + t - 4
+      auto top = [&](int ft) {
+        return as_v8<T>(join(lds_tr8<T>(xt + ft * 16), lds_tr8<T>(xt + 16 * S::XS + ft * 16)));
+      };
+      v8 tring[kPre];
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) tring[i] = top(i);
       if (kb + kBK > k1) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) s[r] = kNegInf;
-      }
-      float mx = kNegInf;
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+          for (int r = 0; r < 4; ++r)
+            if (kb + 16 * mt + 4 * lq + r >= k1) s[mt][r] = kNegInf;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
       if (wave_any(mx > m_run + 8.0f)) {
+        // lazy rescale: only when the running max grows by more than 2^8
         const float m_new = fmaxf(m_run, mx);
         const float alpha = fast_exp2(m_run - m_new);
         m_run = m_new;
@@ -134,36 +159,37 @@ __global__ __launch_bounds__(kThreads, 2) void absorb_fwd_kernel(
 #pragma unroll
         for (int i = 0; i < NF; ++i)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+          for (int r = 0; r < 4; ++r) acc[i][r] *= alpha;
       }
-      float psum = 0.f;
+      v8 pb;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(__builtin_fmaf(s[r], c, -m_run));
-        s[r] = p;
-        psum += p;
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(__builtin_fmaf(s[mt][r], c, -m_run));
+          l_part += p;
+          pb[4 * mt + r] = static_cast<T>(p);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ft = 0; ft < NF; ++ft) {
+        acc[ft] = M16::mma(tring[ft % kPre], pb, acc[ft]);
+        if (ft + kPre < NF) tring[ft % kPre] = top(ft + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      l_part += psum;
-      typename M::v8 pb[2];
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) pb[mm] = pack8<T>(s, mm * 8);
-      // aX^T += X^T P^T with X^T read transposed out of the row-major tile
-#pragma unroll
-      for (int ft = 0; ft < NF; ++ft)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
-          acc[ft] = M::mma(tr_operand<T>(xs, S::XS, mm * 16, ft * 32, lane), pb[mm], acc[ft]);
     }
+    buf = buf == kNBuf - 1 ? 0 : buf + 1;
   }
   wait_vmcnt<0>();
   __syncthreads();
 
   // ---- epilogue: aX/l -> LDS (head-major rows, input dtype), then W_V ----
-  const float l = l_part + __shfl_xor(l_part, 32, 64);
+  float l = l_part + __shfl_xor(l_part, 16, 64);
+  l += __shfl_xor(l, 32, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int TT = kAbsorbRows / H;         // tokens per workgroup
   const int tl = row / H, hh = row % H;   // token / head of this lane's row
-  if (row_ok && lhalf == 0) {
+  if (row_ok && lq == 0) {
     const float lse_v = l > 0.f ? m_run + fast_log2(l) : kNegInf;
     if (pbase < 0)
       lse[(int64_t)t0 * H + row] = lse_v;
@@ -172,39 +198,39 @@ __global__ __launch_bounds__(kThreads, 2) void absorb_fwd_kernel(
   }
   T *axs = smem;  // [kAbsorbRows][XS], row h*TT + t
   if (wave_active) {
-    T *dst = axs + (hh * TT + tl) * S::XS;
+    typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
+    T *dst = axs + (hh * TT + tl) * S::XS + lq * 4;
 #pragma unroll
-    for (int ft = 0; ft < NF; ++ft)
+    for (int ft = 0; ft < NF; ++ft) {
+      T4 w;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-        T4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(row_ok ? acc[ft][g * 4 + e] * inv : 0.f);
-        *reinterpret_cast<T4 *>(dst + ft * 32 + g * 8 + lhalf * 4) = w;
-      }
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(row_ok ? acc[ft][e] * inv : 0.f);
+      *reinterpret_cast<T4 *>(dst + ft * 16) = w;
+    }
   }
   __syncthreads();
-  // projection: per (head, 16-token tile, 16-wide d tile) one 16x16 output
-  const int l16 = lane & 15, lq = lane >> 4;
+  // projection: per (head, 16-token tile, 16-wide d tile) one 16x16 output;
+  // the tile's W_V operands are all requested before the first product
   const int ntok = t1 - t0;
   const int tiles_per_head = (TT + 15) / 16;
   const int n_tiles = H * tiles_per_head * (DH / 16);
-  for (int tile = wave; tile < n_tiles; tile += kWaves) {
+  for (int tile = wave; tile < n_tiles; tile += kFwdWaves) {
     const int dtile = tile % (DH / 16);
     const int tt = (tile / (DH / 16)) % tiles_per_head;
     const int h = tile / ((DH / 16) * tiles_per_head);
     if (tt * 16 >= ntok) continue;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
     const T *arow = axs + (h * TT + tt * 16 + l16) * S::XS + lq * 8;
     const T *brow = wvt + ((int64_t)h * DH + dtile * 16 + l16) * FP + lq * 8;
     const bool a_ok = tt * 16 + l16 < TT;
+    u32x4 bw[NK];
 #pragma unroll
-    for (int kc = 0; kc < FP / 32; ++kc) {
+    for (int kc = 0; kc < NK; ++kc) bw[kc] = *reinterpret_cast<const u32x4 *>(brow + kc * 32);
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < NK; ++kc) {
       const u32x4 a = a_ok ? *reinterpret_cast<const u32x4 *>(arow + kc * 32)
                            : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 b = *reinterpret_cast<const u32x4 *>(brow + kc * 32);
-      o = Mfma16<T>::mma(as_v8<T>(a), as_v8<T>(b), o);
+      o = M16::mma(as_v8<T>(a), as_v8<T>(bw[kc]), o);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -224,7 +250,7 @@ void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   const int smem = AbsSmem<FP>::kBytes;
   hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(kThreads),
+  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(64 * kFwdWaves),
                      smem, st, (const T *)a.u, (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o,
                      a.part_lse, a.items, a.H, a.F, a.scale * kLog2e);
 }

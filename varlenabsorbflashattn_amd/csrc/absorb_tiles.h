@@ -7,11 +7,9 @@
 namespace vafa {
 namespace absorb {
 
-constexpr int kWaves = kAbsorbRows / 32;  // 2 waves x 32 rows
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBK = 32;                   // keys per LDS tile
-constexpr int kNBuf = 3;                  // LDS ring depth
-constexpr int kMaxF = 256;                // D_KV handled by this kernel (padded to 32)
+constexpr int kBK = 32;     // keys per LDS tile
+constexpr int kNBuf = 3;    // LDS ring depth
+constexpr int kMaxF = 256;  // D_KV handled by these kernels (padded to 32)
 
 #ifndef VAFA_ABS_XPAD
 #define VAFA_ABS_XPAD 8
@@ -42,24 +40,23 @@ struct Mfma16<f16> {
   }
 };
 
-// Issue the LDS-DMA loads of one 32-key tile: one instruction per X row,
-// lanes 0..CPR-1 each move one 16-byte chunk to the row's padded LDS slot
-// (keys past k_end and chunks past D_KV arrive as zeros).  Every wave issues
-// kBK / kWaves instructions per tile, which keeps vmcnt accounting uniform.
-template <typename T, int FP>
-__device__ __forceinline__ void issue_tile(const T *__restrict__ X, int kb, int k_end, int F,
-                                           T *tile, int wave, int lane) {
-  using S = AbsSmem<FP>;
-  const int rows = k_end - kb < kBK ? (k_end - kb > 0 ? k_end - kb : 0) : kBK;
-  const u32x4 rx = rsrc_words(X + (int64_t)kb * F, (int64_t)rows * F * 2);
-  // chunks past D_KV get an offset >= 2^31, past any buffer range
+// LDS-DMA of 32 consecutive rows [F] of a row slab (src, bytes) into a
+// padded [32][XS] LDS block (rows past the slab and chunks past F arrive as
+// zeros); each of the workgroup's NW waves moves 32/NW rows, one instruction
+// per row.  The descriptor is rebased per row in scalar registers, so the
+// only per-lane operand is the chunk offset.
+template <int FP, int NW>
+__device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
+                                          int wave, int lane) {
+  constexpr int XS = AbsSmem<FP>::XS;
   const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
-  const uint32_t base = lds_addr(tile);
-  if (lane < S::CPR) {
+  if (lane < FP / 8) {
 #pragma unroll
-    for (int n = 0; n < kBK / kWaves; ++n) {
-      const int r = wave * (kBK / kWaves) + n;
-      lds_dma16(rx, base + r * S::XS * 2, (int32_t)(off + (uint32_t)(r * F * 2)));
+    for (int n = 0; n < 32 / NW; ++n) {
+      const int r = wave * (32 / NW) + n;
+      const int64_t ro = (int64_t)r * F * 2;
+      lds_dma16(rsrc_words(static_cast<const char *>(src) + ro, bytes - ro), base + r * XS * 2,
+                (int32_t)off);
     }
   }
 }

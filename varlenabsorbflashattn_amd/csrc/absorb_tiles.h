@@ -61,25 +61,6 @@ __device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F,
   }
 }
 
-// LDS-address-space views: offsets from one per-lane base fold into the
-// instructions' immediate offsets instead of living in registers.
-template <typename T>
-using lds_cptr = const __attribute__((address_space(3))) T *;
-
-template <typename T>
-__device__ __forceinline__ lds_cptr<T> as_lds(const T *p) {
-  return (lds_cptr<T>)(p);
-}
-template <typename T>
-__device__ __forceinline__ u32x4 lds_ld16(lds_cptr<T> p) {
-  return *(lds_cptr<u32x4>)(p);
-}
-template <typename T>
-__device__ __forceinline__ u32x2 lds_tr8(lds_cptr<T> p) {
-  typedef __attribute__((address_space(3))) v4s16 *tr_ptr;
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((tr_ptr)(p)));
-}
-
 inline int padded_f(int F) { return (F + 31) / 32 * 32; }
 
 }  // namespace absorb

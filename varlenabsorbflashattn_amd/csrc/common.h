@@ -95,6 +95,21 @@ __device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t lds_base, int32_t vo
                : "memory", "m0");
 }
 
+// 4-byte LDS-DMA load: lane l's dword from `rsrc` at byte offset `voff` lands
+// at LDS address lds_base + 4*l (out-of-range offsets write zeros).
+__device__ __forceinline__ void lds_dma4(u32x4 r, uint32_t lds_base, int32_t voff) {
+  typedef uint32_t sgpr4 __attribute__((ext_vector_type(4)));
+  sgpr4 q;
+  q.x = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[0]);
+  q.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[1]);
+  q.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[2]);
+  q.w = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[3]);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(q)
+               : "memory", "m0");
+}
+
 // 32-bit LDS address of a pointer into __shared__ memory.
 template <typename P>
 __device__ __forceinline__ uint32_t lds_addr(const P *p) {

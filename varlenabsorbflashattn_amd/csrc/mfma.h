@@ -70,6 +70,25 @@ __device__ __forceinline__ u32x2 lds_tr16(const T *p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p)));
 }
 
+// LDS-address-space views: offsets from one per-lane base fold into the
+// instructions' immediate offsets instead of living in registers.
+template <typename T>
+using lds_cptr = const __attribute__((address_space(3))) T *;
+
+template <typename T>
+__device__ __forceinline__ lds_cptr<T> as_lds(const T *p) {
+  return (lds_cptr<T>)(p);
+}
+template <typename T>
+__device__ __forceinline__ u32x4 lds_ld16(lds_cptr<T> p) {
+  return *(lds_cptr<u32x4>)(p);
+}
+template <typename T>
+__device__ __forceinline__ u32x2 lds_tr8(lds_cptr<T> p) {
+  typedef __attribute__((address_space(3))) v4s16 *tr_ptr;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((tr_ptr)(p)));
+}
+
 // A operand of a 32x32x16 MFMA whose row index is a column c0 + (l % 32) of
 // a row-major LDS tile (stride elements per row) and whose reduction index
 // runs over tile rows k0 .. k0+15 in the relabelled order of the C layout:

@@ -63,6 +63,23 @@ struct DkvSmem {
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
+// LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
+// past r_end read as zero) into a padded [32][RS] block: wave w moves rows
+// 8w .. 8w+7, one instruction per row with lanes < D/8 active.
+template <typename T, int D>
+__device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
+                                         uint32_t base, int wave, int lane) {
+  constexpr int RS = D + 8;
+  if (lane < D / 8) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int r = wave * 8 + n;
+      const u32x4 rs = rsrc_words(src + ((int64_t)(r0 + r) * H + h) * D, r0 + r < r_end ? D * 2 : 0);
+      lds_dma16(rs, base + r * RS * 2, lane * 16);
+    }
+  }
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
@@ -71,17 +88,35 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     float scale) {
   using M = Mfma<T>;
   using S = DkvSmem<D>;
-  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  constexpr int kPre = D >= 128 ? 2 : 4;  // operand ring depth within the register budget
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int item = blockIdx.x / H, h = blockIdx.x % H;
   const PlanItem it = load_item(items, item);
   const int k0 = it.v[0], k1 = it.v[1], q0 = it.v[2], q1 = it.v[3];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int key = k0 + wave * 32 + lrow;
   const bool key_ok = key < k1;
   const bool wave_active = k0 + wave * 32 < k1;
+
+  // stage query block qb: Q and dO rows by 16-byte DMA, LSE and delta (strided
+  // by H) by one 4-byte DMA per lane -- waves 0/2 LSE, 1/3 delta, so every
+  // wave issues the same count.  Rows past q1 arrive as zeros: Q = dO = 0
+  // there makes both of their products vanish whatever P is.
+  auto issue = [&](int qb, int buf) {
+    unsigned char *base = smem_raw + buf * S::kBufBytes;
+    dma_rows<T, D>(q, qb, q1, H, h, lds_addr(base), wave, lane);
+    dma_rows<T, D>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
+    const float *vec = (wave & 1) ? delta : lse;
+    const int rows = q1 - qb < kRB ? q1 - qb : kRB;
+    const u32x4 rv = rsrc_words(vec + (int64_t)qb * H + h, (int64_t)(rows > 0 ? rows : 0) * H * 4);
+    if (lane < kRB) lds_dma4(rv, lds_addr(base + 2 * S::kQs * 2 + (wave & 1) * kRB * 4), lane * H * 4);
+  };
+  const int nblk = (q1 - q0 + kRB - 1) / kRB;
+  if (nblk > 0) issue(q0, 0);
 
   typename M::v8 kf[NC], vf[NC];
   {
@@ -91,8 +126,11 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
-      kf[cc] = as_v8<T>(buf_load16(rk, off + cc * 32));
-      vf[cc] = as_v8<T>(buf_load16(rv, off + cc * 32));
+      u32x4 a = buf_load16(rk, off + cc * 32), b = buf_load16(rv, off + cc * 32);
+      // waited for here, in the prologue, not inside the loop
+      asm volatile("" : "+v"(a), "+v"(b));
+      kf[cc] = as_v8<T>(a);
+      vf[cc] = as_v8<T>(b);
     }
   }
   f32x16 adk[ND], adv[ND];
@@ -101,86 +139,81 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) adk[i][r] = adv[i][r] = 0.f;
 
-  // threads 0..127 stage Q, 128..255 stage dO; threads < 32 also fetch LSE and
-  // delta (past-the-end rows get LSE=+inf so their P is exactly 0)
-  const bool stage_q = tid < 128;
-  const int st = tid & 127;
-  const T *src = stage_q ? q : dout;
-  Rows<D, 128> stg;
-  float st_lse = 0.f, st_dl = 0.f;
-  auto fetch = [&](int qb) {
-    load_rows<T, D, 128>(stg, src, qb, q1, H, h, st);
-    if (tid < kRB) {
-      const int row = qb + tid;
-      st_lse = row < q1 ? lse[(int64_t)row * H + h] : __builtin_inff();
-      st_dl = row < q1 ? delta[(int64_t)row * H + h] : 0.f;
-    }
-  };
-  auto put = [&](int buf) {
-    unsigned char *base = smem_raw + buf * S::kBufBytes;
-    T *qs = reinterpret_cast<T *>(base);
-    store_rows<T, D, 128>(stg, stage_q ? qs : qs + S::kQs, S::RS, st);
-    float *ls = reinterpret_cast<float *>(base + 2 * S::kQs * 2);
-    if (tid < kRB) {
-      ls[tid] = st_lse;
-      ls[kRB + tid] = st_dl;
-    }
-  };
-
-  const int nblk = (q1 - q0 + kRB - 1) / kRB;
-  if (nblk > 0) {
-    fetch(q0);
-    put(0);
-  }
-  __syncthreads();
+  // per-lane element offsets: row lrow at d = 8*lhalf (A of S and dP) and the
+  // origin of the transposed reads (layout of tr_operand)
+  const int a_off = lrow * RS + lhalf * 8;
+  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+                    4 * (lane & 3);
   for (int j = 0; j < nblk; ++j) {
-    if (j + 1 < nblk) fetch(q0 + (j + 1) * kRB);
-    if (wave_active) {
-      const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
-      const T *qs = reinterpret_cast<const T *>(base);
-      const T *ds_ = qs + S::kQs;
-      const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
-      f32x16 s, dp;
+    wait_vmcnt<0>();
+    __syncthreads();  // block j visible; every wave is done with the other buffer
+    if (j + 1 < nblk) issue(q0 + (j + 1) * kRB, (j + 1) & 1);
+    if (!wave_active) continue;
+    const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
+    const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
+    const lds_cptr<T> ds_ = qs + S::kQs;
+    const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
+    // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
+    auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
+    f32x16 s, dp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+    u32x4 ring[kPre];
 #pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(qs + lrow * S::RS + cc * 16 + lhalf * 8);
-        s = M::mma(as_v8<T>(a), kf[cc], s);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(ds_ + lrow * S::RS + cc * 16 + lhalf * 8);
-        dp = M::mma(as_v8<T>(b), vf[cc], dp);
-      }
+    for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
-        const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = g * 4 + e;
-          const float p = key_ok ? fast_exp2(__builtin_fmaf(s[r], c, -L[e])) : 0.f;
-          s[r] = p;
-          dp[r] = p * (dp[r] - Dl[e]);
-        }
-      }
-      typename M::v8 pb[2], sb[2];
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        pb[mm] = pack8<T>(s, mm * 8);
-        sb[mm] = pack8<T>(dp, mm * 8);
-      }
-#pragma unroll
-      for (int dtile = 0; dtile < ND; ++dtile)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          adv[dtile] = M::mma(tr_operand<T>(ds_, S::RS, mm * 16, dtile * 32, lane), pb[mm],
-                              adv[dtile]);
-          adk[dtile] = M::mma(tr_operand<T>(qs, S::RS, mm * 16, dtile * 32, lane), sb[mm],
-                              adk[dtile]);
-        }
+    for (int i = 0; i < 2 * NC; ++i) {
+      const typename M::v8 a = as_v8<T>(ring[i % kPre]);
+      if (i & 1)
+        dp = M::mma(a, vf[i >> 1], dp);
+      else
+        s = M::mma(a, kf[i >> 1], s);
+      if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (j + 1 < nblk) put((j + 1) & 1);
-    __syncthreads();
+    // transposed operands: i -> d tile i % ND, query half mm = (i / ND) >> 1,
+    // dO^T (for dV^T, with P) when (i / ND) is even, else Q^T (for dK^T, with dS)
+    auto top = [&](int i) {
+      const lds_cptr<T> p =
+          (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
+      return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+    };
+    typename M::v8 tring[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
+      const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = g * 4 + e;
+        const float p = key_ok ? fast_exp2(__builtin_fmaf(s[r], c, -L[e])) : 0.f;
+        s[r] = p;
+        dp[r] = p * (dp[r] - Dl[e]);
+      }
+    }
+    typename M::v8 pb[2], sb[2];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      pb[mm] = pack8<T>(s, mm * 8);
+      sb[mm] = pack8<T>(dp, mm * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4 * ND; ++i) {
+      const int dt = i % ND, q2 = i / ND, mm = q2 >> 1;
+      const typename M::v8 a = tring[i % kPre];
+      if (q2 & 1)
+        adk[dt] = M::mma(a, sb[mm], adk[dt]);
+      else
+        adv[dt] = M::mma(a, pb[mm], adv[dt]);
+      if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  wait_vmcnt<0>();
 
   if (!key_ok) return;
   typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
@@ -225,7 +258,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   const int item = blockIdx.x / H, h = blockIdx.x % H;
   const PlanItem it = load_item(items, item);
   const int q0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int qrow = q0 + wave * 32 + lrow;
   const bool row_ok = qrow < q1;
@@ -239,12 +273,15 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
-      qf[cc] = as_v8<T>(buf_load16(rq, off + cc * 32));
-      dof[cc] = as_v8<T>(buf_load16(rd, off + cc * 32));
+      u32x4 a = buf_load16(rq, off + cc * 32), b = buf_load16(rd, off + cc * 32);
+      asm volatile("" : "+v"(a), "+v"(b));  // waited for in the prologue
+      qf[cc] = as_v8<T>(a);
+      dof[cc] = as_v8<T>(b);
     }
   }
-  const float Lr = row_ok ? lse[(int64_t)qrow * H + h] : __builtin_inff();
-  const float Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+  float Lr = row_ok ? lse[(int64_t)qrow * H + h] : __builtin_inff();
+  float Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+  asm volatile("" : "+v"(Lr), "+v"(Dr));
   f32x16 acc[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i)
@@ -252,7 +289,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
   // threads 0..127 stage K, 128..255 stage V (both row-major)
-  const bool stage_k = tid < 128;
+  const bool stage_k = wave < 2;
   const int st = tid & 127;
   const T *src = stage_k ? k : v;
   Rows<D, 128> stg;

@@ -4,14 +4,17 @@
 // from the forward's log2-domain LSE (fa/kernels.py:233-494):
 //   * dK/dV, key-major: a workgroup owns 128 keys of one head (32 per wave,
 //     K and V held in registers as MFMA operands) and walks the segment's
-//     queries in blocks of 32 staged row-major in LDS (the transposed
-//     operands Q^T, dO^T come from ds_read_b64_tr_b16):
+//     queries in blocks of 32 staged row-major in LDS by buffer_load ... lds,
+//     double-buffered (the transposed operands Q^T, dO^T come from
+//     ds_read_b64_tr_b16):
 //       S = Q K^T, dP = dO V^T, dS = P (dP - delta),
 //       dV^T += dO^T P,  dK^T += Q^T dS           (4 products per block)
 //   * dQ, query-major over the forward's plan items (including split-K
 //     partials): S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
-// The row statistics of the dQ kernel stay per lane (lane <-> query row);
-// the dK/dV kernel reads LSE and delta of its 32-row block from LDS.
+// The dQ kernel stages K / V blocks through registers.  Its row statistics stay
+// per lane (lane <-> query row); the dK/dV kernel reads LSE and delta of its
+// 32-row block from LDS.  LDS operands are read a few products ahead of the
+// MFMAs that consume them (sched_barrier keeps that order).
 #include "kernels.h"
 #include "mfma.h"
 
@@ -20,40 +23,6 @@ namespace vafa {
 namespace {
 
 constexpr int kRB = 32;  // rows per staged block (queries for dK/dV, keys for dQ)
-
-// A [kRB x D] block of a [T, H, D] tensor staged through registers: 16-byte
-// chunks, rows past the buffer range read as zero.
-template <int D, int NT>
-struct Rows {
-  static constexpr int kChunks = kRB * D / 8;
-  static constexpr int kPer = (kChunks + NT - 1) / NT;
-  u32x4 v[kPer];
-};
-
-template <typename T, int D, int NT>
-__device__ __forceinline__ void load_rows(Rows<D, NT> &s, const T *__restrict__ src, int r0,
-                                          int r_end, int H, int h, int t) {
-  constexpr int CPR = D / 8;
-  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
-  const rsrc_t rs = make_rsrc(src + (int64_t)r0 * H * D, (int64_t)rows * H * D * 2);
-#pragma unroll
-  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
-    const int ci = t + NT * i;
-    const int row = ci < Rows<D, NT>::kChunks ? ci / CPR : kRB;
-    s.v[i] = buf_load16(rs, (row * H + h) * D * 2 + (ci % CPR) * 16);
-  }
-}
-
-template <typename T, int D, int NT>
-__device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int RS, int t) {
-  constexpr int CPR = D / 8;
-#pragma unroll
-  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
-    const int ci = t + NT * i;
-    if (ci < Rows<D, NT>::kChunks)
-      *reinterpret_cast<u32x4 *>(dst + (ci / CPR) * RS + (ci % CPR) * 8) = s.v[i];
-  }
-}
 
 template <int D>
 struct DkvSmem {
@@ -235,6 +204,40 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     }
 }
 
+// A [kRB x D] block of a [T, H, D] tensor staged through registers: 16-byte
+// chunks, rows past the buffer range read as zero.
+template <int D, int NT>
+struct Rows {
+  static constexpr int kChunks = kRB * D / 8;
+  static constexpr int kPer = (kChunks + NT - 1) / NT;
+  u32x4 v[kPer];
+};
+
+template <typename T, int D, int NT>
+__device__ __forceinline__ void load_rows(Rows<D, NT> &s, const T *__restrict__ src, int r0,
+                                          int r_end, int H, int h, int t) {
+  constexpr int CPR = D / 8;
+  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
+  const rsrc_t rs = make_rsrc(src + (int64_t)r0 * H * D, (int64_t)rows * H * D * 2);
+#pragma unroll
+  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
+    const int ci = t + NT * i;
+    const int row = ci < Rows<D, NT>::kChunks ? ci / CPR : kRB;
+    s.v[i] = buf_load16(rs, (row * H + h) * D * 2 + (ci % CPR) * 16);
+  }
+}
+
+template <typename T, int D, int NT>
+__device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int RS, int t) {
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
+    const int ci = t + NT * i;
+    if (ci < Rows<D, NT>::kChunks)
+      *reinterpret_cast<u32x4 *>(dst + (ci / CPR) * RS + (ci % CPR) * 8) = s.v[i];
+  }
+}
+
 template <int D>
 struct DqSmem {
   static constexpr int RS = D + 8;
@@ -251,7 +254,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     float c, float scale) {
   using M = Mfma<T>;
   using S = DqSmem<D>;
-  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  constexpr int kPre = 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
@@ -264,6 +268,21 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   const int qrow = q0 + wave * 32 + lrow;
   const bool row_ok = qrow < q1;
   const bool wave_active = q0 + wave * 32 < q1;
+
+  // key blocks staged through registers (waves 0-1 K, 2-3 V; rows past k1
+  // read as zero): a block's loads are issued before the previous block's
+  // compute and written to LDS after it.  (Per-row LDS-DMA moves only D*2
+  // bytes per instruction, which costs more than it saves here.)
+  const bool stage_k = wave < 2;
+  const int st = tid & 127;
+  const T *src = stage_k ? k : v;
+  Rows<D, 128> stg;
+  auto put = [&](int buf) {
+    T *ks = smem + buf * S::kBuf;
+    store_rows<T, D, 128>(stg, stage_k ? ks : ks + S::kKs, RS, st);
+  };
+  const int nblk = (k1 - k0 + kRB - 1) / kRB;
+  if (nblk > 0) load_rows<T, D, 128>(stg, src, k0, k1, H, h, st);
 
   typename M::v8 qf[NC], dof[NC];
   {
@@ -288,37 +307,45 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-  // threads 0..127 stage K, 128..255 stage V (both row-major)
-  const bool stage_k = wave < 2;
-  const int st = tid & 127;
-  const T *src = stage_k ? k : v;
-  Rows<D, 128> stg;
-  const int nblk = (k1 - k0 + kRB - 1) / kRB;
-  auto put = [&](int buf) {
-    T *ks = smem + buf * S::kBuf;
-    store_rows<T, D, 128>(stg, stage_k ? ks : ks + S::kKs, S::RS, st);
-  };
-  if (nblk > 0) {
-    load_rows<T, D, 128>(stg, src, k0, k1, H, h, st);
-    put(0);
-  }
+  const int a_off = lrow * RS + lhalf * 8;
+  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+                    4 * (lane & 3);
+  if (nblk > 0) put(0);
   __syncthreads();
   for (int j = 0; j < nblk; ++j) {
     const int kb = k0 + j * kRB;
     if (j + 1 < nblk) load_rows<T, D, 128>(stg, src, kb + kRB, k1, H, h, st);
     if (wave_active) {
-      const T *ks = smem + (j & 1) * S::kBuf;
-      const T *vs = ks + S::kKs;
+      const lds_cptr<T> ks = as_lds(smem + (j & 1) * S::kBuf);
+      const lds_cptr<T> vs = ks + S::kKs;
+      // S^T = K Q^T (even reads, K rows) and dP^T = V dO^T (odd reads, V rows)
+      auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? vs : ks) + a_off + (i >> 1) * 16); };
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+      u32x4 ring[kPre];
 #pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(ks + lrow * S::RS + cc * 16 + lhalf * 8);
-        s = M::mma(as_v8<T>(a), qf[cc], s);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(vs + lrow * S::RS + cc * 16 + lhalf * 8);
-        dp = M::mma(as_v8<T>(b), dof[cc], dp);
+      for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 2 * NC; ++i) {
+        const typename M::v8 a = as_v8<T>(ring[i % kPre]);
+        if (i & 1)
+          dp = M::mma(a, dof[i >> 1], dp);
+        else
+          s = M::mma(a, qf[i >> 1], s);
+        if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      // K^T operands of dQ^T: i -> d tile i % ND, key half i / ND
+      auto top = [&](int i) {
+        const lds_cptr<T> p = ks + t_off + (i / ND) * 16 * RS + (i % ND) * 32;
+        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+      };
+      typename M::v8 tring[kPre];
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+      // element r holds key kb + (r/4)*8 + lhalf*4 + r%4 of this lane's row
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lr));
@@ -332,12 +359,13 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
       typename M::v8 sb[2];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) sb[mm] = pack8<T>(dp, mm * 8);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int dtile = 0; dtile < ND; ++dtile)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
-          acc[dtile] = M::mma(tr_operand<T>(ks, S::RS, mm * 16, dtile * 32, lane), sb[mm],
-                              acc[dtile]);
+      for (int i = 0; i < 2 * ND; ++i) {
+        acc[i % ND] = M::mma(tring[i % kPre], sb[i / ND], acc[i % ND]);
+        if (i + kPre < 2 * ND) tring[i % kPre] = top(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     if (j + 1 < nblk) put((j + 1) & 1);
     __syncthreads();

@@ -15,7 +15,8 @@ from typing import Optional
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libvafa.so")
+# VAFA_LIBRARY selects another build of the library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("VAFA_LIBRARY") or os.path.join(_HERE, "libvafa.so")
 
 VAFA_OK = 0
 VAFA_ERR_VALUE = -1

@@ -23,10 +23,14 @@ namespace vafa {
 namespace {
 
 constexpr int kRB = 32;  // rows per staged block (queries for dK/dV, keys for dQ)
+#ifndef VAFA_VPAD
+#define VAFA_VPAD 24
+#endif
+constexpr int kPad = VAFA_VPAD;  // LDS row padding (elements)
 
 template <int D>
 struct DkvSmem {
-  static constexpr int RS = D + 8;
+  static constexpr int RS = D + kPad;
   static constexpr int kQs = kRB * RS;                        // Q (or dO) row-major
   static constexpr int kBufBytes = 2 * kQs * 2 + 2 * kRB * 4;  // Q, dO, LSE, delta
   static constexpr int kBytes = 2 * kBufBytes;
@@ -38,7 +42,7 @@ struct DkvSmem {
 template <typename T, int D>
 __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
                                          uint32_t base, int wave, int lane) {
-  constexpr int RS = D + 8;
+  constexpr int RS = D + kPad;
   if (lane < D / 8) {
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
@@ -240,7 +244,7 @@ __device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int RS,
 
 template <int D>
 struct DqSmem {
-  static constexpr int RS = D + 8;
+  static constexpr int RS = D + kPad;
   static constexpr int kKs = kRB * RS;
   static constexpr int kBuf = 2 * kKs;  // K and V row-major
   static constexpr int kBytes = 2 * kBuf * 2;

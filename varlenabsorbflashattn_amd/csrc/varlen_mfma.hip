@@ -18,7 +18,10 @@ namespace {
 
 constexpr int kBM = kVarlenQTile;  // 128 query rows per workgroup
 constexpr int kBN = 64;            // keys per LDS tile
-constexpr int kKPad = 8;           // K row padding (elements)
+#ifndef VAFA_VPAD
+#define VAFA_VPAD 24
+#endif
+constexpr int kKPad = VAFA_VPAD;   // K / V row padding (elements)
 
 template <int D>
 struct FwdSmem {

@@ -18,15 +18,21 @@ namespace {
 
 constexpr int kBM = kVarlenQTile;  // 128 query rows per workgroup
 constexpr int kBN = 64;            // keys per LDS tile
-#ifndef VAFA_VPAD
-#define VAFA_VPAD 24
-#endif
-constexpr int kKPad = VAFA_VPAD;   // K / V row padding (elements)
+// LDS row padding (elements).  K is read by ds_read_b128 (rows as the A
+// operand) and V only by ds_read_b64_tr_b16 (V^T operands); measured on
+// gfx950 the two want different row strides: 16-byte row reads are
+// conflict-free when the stride is 8 * odd elements (D + 24), the transposed
+// reads when it is 32 mod 128 elements (D + 32).
+constexpr int kKPad = 24;
+constexpr int kVPad = 32;
 
 template <int D>
 struct FwdSmem {
-  static constexpr int kKs = kBN * (D + kKPad);  // elements per K (or V) buffer
-  static constexpr int kBuf = 2 * kKs;           // K and V, both row-major
+  static constexpr int KSK = D + kKPad;          // K row stride (elements)
+  static constexpr int KSV = D + kVPad;          // V row stride (elements)
+  static constexpr int kKs = kBN * KSK;          // elements per K buffer
+  static constexpr int kVs = kBN * KSV;          // elements per V buffer
+  static constexpr int kBuf = kKs + kVs;         // K then V
   static constexpr int kBytes = 2 * kBuf * 2;    // double buffered, 2 B/elt
 };
 
@@ -65,13 +71,12 @@ __device__ __forceinline__ void load_tile(TileRegs<D> &r, const T *__restrict__ 
 template <typename T, int D>
 __device__ __forceinline__ void store_tile(const TileRegs<D> &r, T *ks, T *vs, int tid) {
   constexpr int CPR = D / 8;
-  constexpr int KS = D + kKPad;
 #pragma unroll
   for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
     const int ci = tid + 256 * i;
     const int key = ci / CPR, dc = ci % CPR;
-    *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = r.kc[i];
-    *reinterpret_cast<u32x4 *>(vs + key * KS + dc * 8) = r.vc[i];
+    *reinterpret_cast<u32x4 *>(ks + key * FwdSmem<D>::KSK + dc * 8) = r.kc[i];
+    *reinterpret_cast<u32x4 *>(vs + key * FwdSmem<D>::KSV + dc * 8) = r.vc[i];
   }
 }
 
@@ -90,7 +95,7 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
                                          float c, int kbase, int k_end, int lane) {
   using M = Mfma<T>;
   constexpr int NC = D / 16, ND = D / 32;
-  constexpr int KS = D + kKPad;
+  constexpr int KS = FwdSmem<D>::KSK, VS = FwdSmem<D>::KSV;
   const int lrow = lane & 31, lhalf = lane >> 5;
   // S^T for the two 32-key halves as two interleaved MFMA chains; K operands
   // are read kPre steps ahead so LDS latency hides behind earlier MFMAs.
@@ -161,7 +166,7 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
   constexpr int NP = 4 * ND;
   auto vop = [&](int i) {  // i = km * ND + dt, km = kt * 2 + mm
     const int km = i / ND, dt = i % ND;
-    return tr_operand<T>(vs, KS, km * 16, dt * 32, lane);
+    return tr_operand<T>(vs, VS, km * 16, dt * 32, lane);
   };
   typename M::v8 vring[kPre];
 #pragma unroll

@@ -38,17 +38,22 @@ struct DkvSmem {
 
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
 // past r_end read as zero) into a padded [32][RS] block: wave w moves rows
-// 8w .. 8w+7, one instruction per row with lanes < D/8 active.
+// 8w .. 8w+7, one instruction per row with lanes < D/8 active.  One buffer
+// descriptor covers the block's valid rows; the row sits in the lane offset.
 template <typename T, int D>
 __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
                                          uint32_t base, int wave, int lane) {
   constexpr int RS = D + kPad;
+  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
+  const u32x4 rs = rsrc_words(src + (int64_t)r0 * H * D, (int64_t)(rows > 0 ? rows : 0) * H * D * 2);
+  const int off = (wave * 8 * H + h) * D * 2 + lane * 16;
   if (lane < D / 8) {
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const int r = wave * 8 + n;
-      const u32x4 rs = rsrc_words(src + ((int64_t)(r0 + r) * H + h) * D, r0 + r < r_end ? D * 2 : 0);
-      lds_dma16(rs, base + r * RS * 2, lane * 16);
+      // one add of a scalar row term (volatile: not hoisted into 8 registers)
+      int voff;
+      asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(n * H * D * 2), "v"(off));
+      lds_dma16(rs, base + (wave * 8 + n) * RS * 2, voff);
     }
   }
 }
@@ -162,7 +167,9 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = g * 4 + e;
-        const float p = key_ok ? fast_exp2(__builtin_fmaf(s[r], c, -L[e])) : 0.f;
+        // keys past k1 have zero K and V rows; their dK / dV columns are
+        // never stored, so their P needs no masking
+        const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
         s[r] = p;
         dp[r] = p * (dp[r] - Dl[e]);
       }

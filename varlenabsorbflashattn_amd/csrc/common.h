@@ -68,7 +68,9 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t byte_off) {
 // land at LDS address lds_base + 16*l (out-of-range offsets write zeros).
 // Written as inline asm so that the compiler's automatic waits do not treat
 // every later LDS read as dependent on it; callers order it with explicit
-// s_waitcnt vmcnt(N) + barrier.
+// s_waitcnt vmcnt(N) + barrier.  An SALU write of M0 needs one wait state
+// before an LDS-DMA instruction reads it, and the compiler does not pad
+// inside inline asm, hence the s_nop.
 // Raw buffer descriptor words (base, stride 0, num_records, gfx9 flags) for
 // use in inline asm.
 __device__ __forceinline__ u32x4 rsrc_words(const void *base, int64_t bytes) {
@@ -89,7 +91,7 @@ __device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t lds_base, int32_t vo
   q.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[1]);
   q.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[2]);
   q.w = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[3]);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(lds_base), "v"(voff), "s"(q)
                : "memory", "m0");
@@ -104,7 +106,7 @@ __device__ __forceinline__ void lds_dma4(u32x4 r, uint32_t lds_base, int32_t vof
   q.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[1]);
   q.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[2]);
   q.w = (uint32_t)__builtin_amdgcn_readfirstlane((int)r[3]);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                :
                : "s"(lds_base), "v"(voff), "s"(q)
                : "memory", "m0");

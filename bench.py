@@ -94,6 +94,81 @@ def bench_varlen_c2(steps, warmup):
     return case, ms, fwd_ms, flops, dkv_ms
 
 
+def bench_varlen_case(case, steps, warmup):
+    """fwd+bwd ms/step (wall clock around synchronized steps) and fwd ms (HIP events)."""
+    import torch
+    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
+    dev = torch.device("cuda:0")
+    q, k, v, do = W.varlen_tensors(case, dev, with_grad_out=True)
+    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
+    q.requires_grad_(True), k.requires_grad_(True), v.requires_grad_(True)
+
+    def step():
+        o = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+        o.backward(do)
+        q.grad = k.grad = v.grad = None
+
+    def fwd():
+        with torch.no_grad():
+            packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    fwd_ms = time_region(fwd, steps)
+    del q, k, v, do
+    torch.cuda.empty_cache()
+    return ms, fwd_ms
+
+
+def replay_records():
+    """Production lengths sampled from the reference's fixtures
+    (fa-fix/stage1_shapes.jsonl, ta-fix/real_shape_all.json) into tests/golden."""
+    g = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden")
+    with open(os.path.join(g, "stage1_shapes_subset.jsonl")) as f:
+        stage1 = [json.loads(line) for line in f if line.strip()]
+    with open(os.path.join(g, "ta_real_shape_subset.json")) as f:
+        ta = json.load(f)["records"]
+    return stage1, ta
+
+
+def bench_replay(steps, warmup):
+    """Varlen fwd / fwd+bwd on the stage-1 serving shapes at H=4, D=64
+    (fa-tools/benchmark_packed_varlen_flash_attn.py:900-954) and the absorb
+    inner op on the real target-attention shapes, d_q=968, d_kv=216
+    (ta/test_smoke.py:467-534), bf16."""
+    import torch
+    from varlenabsorbflashattn_amd import workloads as W
+    stage1, ta = replay_records()
+    out = {"config": "replay", "stage1_H4_D64": [], "ta_real_dq968_dkv216": []}
+    for r in stage1:
+        case = W.VarlenCase(r["name"], r["q_lens"], r["k_lens"], 4, 64, torch.bfloat16)
+        ms, fwd_ms = bench_varlen_case(case, steps, warmup)
+        out["stage1_H4_D64"].append({
+            "name": r["name"], "segments": len(r["q_lens"]), "sum_lq": int(sum(r["q_lens"])),
+            "sum_lk": int(sum(r["k_lens"])), "fwd_ms": fwd_ms,
+            "fwd_TFLOP/s": case.flops_fwd / (fwd_ms * 1e-3) / 1e12, "fwd_bwd_ms": ms,
+            "fwd_bwd_TFLOP/s": (case.flops_fwd + case.flops_bwd) / (ms * 1e-3) / 1e12})
+        log(out["stage1_H4_D64"][-1])
+    for r in ta:
+        case = W.AbsorbCase(r["tag"], r["q_lens"], r["k_lens"], 8, 32, int(r["d_kv"]),
+                            torch.bfloat16)
+        a_ms = bench_absorb(case, max(steps, 3), d_q=int(r["d_q"]))
+        b_ms, bf_ms = bench_absorb_bwd(case, max(steps, 3), d_q=int(r["d_q"]))
+        gbs = case.bytes_fwd() / (a_ms * 1e-3) / 1e9
+        out["ta_real_dq968_dkv216"].append({
+            "name": r["tag"], "samples": len(r["q_lens"]), "sum_lq": int(sum(r["q_lens"])),
+            "sum_lk": int(sum(r["k_lens"])), "fwd_ms": a_ms, "fwd_GB/s": gbs,
+            "fwd_hbm_frac": gbs / HBM_PEAK_GBS, "fwd_bwd_ms": b_ms})
+        log(out["ta_real_dq968_dkv216"][-1])
+    return out
+
+
 def bench_varlen_c3(iters):
     import torch
     from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
@@ -113,7 +188,7 @@ def bench_varlen_c3(iters):
     return case, ms
 
 
-def bench_absorb(case, iters):
+def bench_absorb(case, iters, d_q=None):
     """Inner absorb forward on precomputed u, through the reference's hot-path
     contract: prepare_target_attn_indices once, then validate=False calls
     (ta/interface.py:125-138) -- no host round trip inside the timed loop."""
@@ -122,7 +197,7 @@ def bench_absorb(case, iters):
     from varlenabsorbflashattn_amd import workloads as W
     from varlenabsorbflashattn_amd.absorb import _project_u
     dev = torch.device("cuda:0")
-    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev)
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev, d_q=d_q)
     cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
     with torch.no_grad():
         u = _project_u(q_raw, W_Q, W_K).contiguous()
@@ -140,7 +215,7 @@ def bench_absorb(case, iters):
     return ms
 
 
-def bench_absorb_bwd(case, iters):
+def bench_absorb_bwd(case, iters, d_q=None):
     """Inner absorb forward + backward (grads of u, X, W_V) on precomputed u,
     validate=False, with a fixed synthetic dO; returns (fwd+bwd ms, fwd ms)."""
     import torch
@@ -148,7 +223,7 @@ def bench_absorb_bwd(case, iters):
     from varlenabsorbflashattn_amd import workloads as W
     from varlenabsorbflashattn_amd.absorb import _project_u
     dev = torch.device("cuda:0")
-    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev)
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev, d_q=d_q)
     cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
     with torch.no_grad():
         u = _project_u(q_raw, W_Q, W_K).contiguous()
@@ -237,6 +312,8 @@ def run_only(which, steps, warmup):
     if which == "c3":
         case, ms = bench_varlen_c3(max(steps, 1))
         return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+    if which == "replay":
+        return bench_replay(max(steps, 1), warmup)
     if which == "c4b":
         case = W.config4(seed=0)
         ms, f_ms = bench_absorb_bwd(case, max(steps, 1))
@@ -253,7 +330,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4b", "c5", "copy"],
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4b", "c5", "copy", "replay"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:

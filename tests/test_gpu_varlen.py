@@ -212,3 +212,19 @@ def test_backward_stages_match_fused(device):
     torch.cuda.synchronize()
     assert torch.equal(st.o, o.detach())
     assert torch.equal(st.dq, qq.grad) and torch.equal(st.dk, kk.grad) and torch.equal(st.dv, vv.grad)
+
+
+def test_stage1_real_shape(device):
+    """A production stage-1 shape (fa-fix/stage1_shapes.jsonl, sampled into
+    tests/golden): 500 queries per user against up to 102400 keys at H=4,
+    D=64, so every tile runs the 4096-key split path and the LSE combine."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "stage1_shapes_subset.jsonl")
+    with open(path) as f:
+        rec = json.loads(f.readline())
+    q_lens, k_lens = rec["q_lens"][:3], rec["k_lens"][:3]
+    print(f"[varlen stage1] {rec['name']} q={q_lens} k={k_lens}", flush=True)
+    got, ref = run_case(q_lens, k_lens, 4, 64, torch.bfloat16, device)
+    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(n, a, r)

@@ -98,6 +98,7 @@ typedef struct vafa_plan_info {
   int64_t plan_ints;              /* total plan length in int32            */
   int64_t q_tile, k_tile;         /* tile sizes the plan was built for     */
   int64_t max_split;              /* largest number of splits of one tile  */
+  int64_t max_comb_rows;          /* most rows (tokens) of one combine item */
 } vafa_plan_info;
 
 /* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).

@@ -136,6 +136,8 @@ def check_varlen_plan(q_lens, k_lens, H=4, D=64):
     assert not cover
     # 2) split partial rows are disjoint, contiguous per tile, inside n_part_rows
     used = np.zeros(p.info.n_part_rows, dtype=np.int64)
+    # the combine launch sizes its grid by the longest combine item
+    assert p.info.max_comb_rows == max([q1 - q0 for q0, q1, *_ in comb.tolist()], default=0)
     for q0, q1, pbase, ns, seg, *_ in comb.tolist():
         R = q1 - q0
         slots = sorted((r[4], r[6]) for r in fwd.tolist() if r[0] == q0 and r[1] == q1)
@@ -214,6 +216,8 @@ def check_absorb_plan(q_lens, k_lens, H=8):
     for t0, t1, k0, k1, pb, seg, *_ in qt.tolist():
         r = sorted(cover[(t0, t1)])
         assert r[0][0] == k0 == ck[seg] and r[-1][1] == k1 == ck[seg + 1]
+    comb = p.section("comb").tolist()
+    assert p.info.max_comb_rows == max([t1 - t0 for t0, t1, *_ in comb], default=0)
     keys = np.zeros(int(ck[-1]), dtype=np.int64)
     for k0, k1, t0, t1, seg, *_ in p.section("kv").tolist():
         keys[k0:k1] += 1

@@ -81,7 +81,8 @@ void varlen_fwd_dispatch(const VarlenArgs &a, hipStream_t st) {
 template <typename T>
 void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
   varlen_fwd_dispatch<T>(a, st);
-  launch_lse_combine<T>(a.part_o, a.part_lse, a.o, a.lse, a.comb_items, a.n_comb, a.H, a.D, st);
+  launch_lse_combine<T>(a.part_o, a.part_lse, a.o, a.lse, a.comb_items, a.n_comb, a.H, a.D,
+                        a.comb_rows, st);
 }
 
 // Backward stages.  Matrix-core kernels for D in {32, 64, 128}; D=16 and
@@ -101,7 +102,7 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
       }
     }
     if (!mfma) launch_simt_varlen_dq<T>(a, st);
-    launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, st);
+    launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, a.comb_rows, st);
   } else {
     if constexpr (sizeof(T) == 2) {
       if (mfma) {
@@ -163,7 +164,8 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
   } else {
     launch_simt_absorb_fwd<T>(a, st);
   }
-  launch_lse_combine<T>(a.part_o, a.part_lse, a.O, a.lse, a.comb_items, a.n_comb, a.H, a.DH, st);
+  launch_lse_combine<T>(a.part_o, a.part_lse, a.O, a.lse, a.comb_items, a.n_comb, a.H, a.DH,
+                        a.comb_rows, st);
 }
 
 template <typename T>
@@ -238,6 +240,7 @@ int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float 
   a.part_o = w.part_o; a.part_lse = w.part_lse;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   if (int rc = by_dtype<VFwd>(dtype, a, (hipStream_t)stream)) return rc;
@@ -264,6 +267,7 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   a.delta = w.delta; a.part_o = w.part_o;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   a.stage = stage;
@@ -325,6 +329,7 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;
@@ -351,6 +356,7 @@ int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O
   a.n_tchunks = w.n_tchunks; a.tchunk = w.tchunk;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;

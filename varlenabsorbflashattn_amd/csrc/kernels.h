@@ -16,6 +16,7 @@ struct VarlenArgs {
   float *part_lse;       // split partial LSE [rows, H] (fwd)
   const int32_t *items, *comb_items, *kv_items;
   int64_t n_items, n_comb, n_kv;
+  int comb_rows;         // most rows of one combine item
   int64_t T_q;
   int H, D;
   float scale;
@@ -35,6 +36,7 @@ struct AbsorbArgs {
   void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
   const int32_t *items, *comb_items, *kv_items, *qseg_items;
   int64_t n_items, n_comb, n_kv, n_qseg;
+  int comb_rows;              // most tokens of one combine item
   int64_t T_q, T_k;
   int64_t n_tchunks, tchunk;
   int H, F, DH;
@@ -54,14 +56,16 @@ template <typename T> void launch_simt_absorb_dx(const AbsorbArgs &, hipStream_t
 template <typename T>
 void launch_row_dot(const void *o, const void *dout, float *delta, int64_t rows, int D,
                     hipStream_t);
-// LSE-weighted merge of split partials into out / lse (fa/kernels.py:652-734)
+// LSE-weighted merge of split partials into out / lse (fa/kernels.py:652-734);
+// every combine item covers at most max_rows rows, D <= 256
 template <typename T>
 void launch_lse_combine(const float *part_o, const float *part_lse, void *out, float *lse,
-                        const int32_t *comb_items, int64_t n_comb, int H, int D, hipStream_t);
+                        const int32_t *comb_items, int64_t n_comb, int H, int D, int max_rows,
+                        hipStream_t);
 // Plain ordered sum of split partials (dQ): out = sum_s part[s]
 template <typename T>
 void launch_sum_combine(const float *part, void *out, const int32_t *comb_items, int64_t n_comb,
-                        int H, int D, hipStream_t);
+                        int H, int D, int max_rows, hipStream_t);
 // dW_V = sum_t aX[t]^T dO[t] per head, two-level deterministic reduction.
 template <typename T>
 void launch_absorb_dwv(const AbsorbArgs &, hipStream_t);

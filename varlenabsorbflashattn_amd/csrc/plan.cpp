@@ -123,6 +123,10 @@ int emit(const std::vector<Item> &sec0, const std::vector<Item> &sec1,
   info->n_fwd = (int64_t)sec0.size();
   info->off_comb = info->off_fwd + info->n_fwd * VAFA_ITEM_INTS;
   info->n_comb = (int64_t)sec1.size();
+  // combine items start {q0, q1, ...} in both plans
+  info->max_comb_rows = 0;
+  for (const Item &it : sec1)
+    info->max_comb_rows = std::max<int64_t>(info->max_comb_rows, it.v[1] - it.v[0]);
   info->off_kv = info->off_comb + info->n_comb * VAFA_ITEM_INTS;
   info->n_kv = (int64_t)sec2.size();
   info->off_qt = info->off_kv + info->n_kv * VAFA_ITEM_INTS;

@@ -34,52 +34,149 @@ __global__ __launch_bounds__(256) void row_dot_kernel(const T *__restrict__ o,
   if (r < rows && part == 0) delta[r] = s;
 }
 
-// Split-K merge in the log2 domain (fa/kernels.py:639-647):
+// Split-K merges.  One wave per (row of a split tile, head) and kCombRows
+// rows per block: the splits' LSEs are read one per lane, then the partial
+// rows are streamed with the lanes along d and eight splits' loads in
+// flight, accumulated in split order (a fixed order, so results repeat bit
+// for bit).  A thread-per-element form re-reads every
+// LSE per element and walks the splits with one dependent load at a time.
+constexpr int kCombRows = 4;
+constexpr int kCombMaxD = 256;                 // d = lane + 64 k, k < kCombMaxD / 64
+constexpr int kCombBatch = 8;                  // split loads in flight per lane
+
+// Log2-domain merge (fa/kernels.py:639-647):
 //   m = max_s lse_s, w_s = exp2(lse_s - m), O = sum_s w_s O_s / sum_s w_s,
-//   LSE = m + log2(sum_s w_s); every split of a tile is non-empty.
-template <typename T>
-__global__ __launch_bounds__(256) void lse_combine_kernel(
+//   LSE = m + log2(sum_s w_s); all splits masked gives O = 0, LSE = -inf.
+// RPW rows per wave: with D <= 32 each half-wave takes its own row, so a
+// wave still moves 64 lanes' worth of every partial.
+template <typename T, int RPW>
+__global__ __launch_bounds__(64 * kCombRows) void lse_combine_kernel(
     const float *__restrict__ part_o, const float *__restrict__ part_lse, T *__restrict__ out,
-    float *__restrict__ lse, const int32_t *__restrict__ items, int H, int D) {
-  const int item = blockIdx.x / H, h = blockIdx.x % H;
+    float *__restrict__ lse, const int32_t *__restrict__ items, int H, int D, int rblocks) {
+  constexpr int CH = 64 / RPW;                           // lanes (and splits) per row group
+  constexpr int KD = RPW == 1 ? kCombMaxD / 64 : 1;      // d = lg + CH k
+  const int lane = threadIdx.x & 63;
+  const int g = lane / CH, lg = lane % CH;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int rb = (int)blockIdx.x % rblocks, ih = (int)blockIdx.x / rblocks;
+  const int item = ih / H, h = ih - item * H;
   const PlanItem it = load_item(items, item);
   const int q0 = it.v[0], q1 = it.v[1], pbase = it.v[2], ns = it.v[3];
   const int R = q1 - q0;
-  for (int idx = threadIdx.x; idx < R * D; idx += 256) {
-    const int r = idx / D, d = idx % D;
-    float m = kNegInf;
-    for (int s = 0; s < ns; ++s)
-      m = fmaxf(m, part_lse[(int64_t)(pbase + s * R + r) * H + h]);
-    const float ms = m == kNegInf ? 0.f : m;
-    float l = 0.f, acc = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const int64_t pr = (int64_t)(pbase + s * R + r) * H + h;
-      const float w = fast_exp2(part_lse[pr] - ms);
-      l += w;
-      acc += w * part_o[pr * D + d];
+  const int r0 = (rb * kCombRows + wave) * RPW;  // the wave's first row
+  if (r0 >= R) return;
+  const int r = r0 + g;
+  const bool row_ok = r < R;
+  auto prow = [&](int sp) { return (int64_t)(pbase + sp * R + r) * H + h; };
+  // lane g*CH + s of a chunk holds split s of row group g; readlane
+  // broadcasts it (scalar, no LDS round trip) and keeps sums in split order
+  auto bcast = [&](float x, int j) {
+    float y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+    if (RPW == 2) {
+      const float yb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), CH + j));
+      y = g ? yb : y;
     }
-    const float ls = l == 0.f ? 1.f : l;
-    out[((int64_t)(q0 + r) * H + h) * D + d] = from_f<T>(acc / ls);
-    if (d == 0) lse[(int64_t)(q0 + r) * H + h] = m == kNegInf ? kNegInf : ms + fast_log2(ls);
+    return y;
+  };
+  auto load_batch = [&](int s0, int nc, int j0, float (&v)[kCombBatch][KD]) {
+#pragma unroll
+    for (int jj = 0; jj < kCombBatch; ++jj)
+#pragma unroll
+      for (int k = 0; k < KD; ++k) {
+        const int d = lg + CH * k;
+        v[jj][k] = (row_ok && j0 + jj < nc && d < D) ? part_o[prow(s0 + j0 + jj) * D + d] : 0.f;
+      }
+  };
+  // The first chunk's LSEs and its first batch of partial rows are requested
+  // together (the rows do not depend on the max), so a row with at most
+  // kCombBatch splits costs one memory round trip.
+  const int nc0 = ns < CH ? ns : CH;
+  const float x0 = (row_ok && lg < nc0) ? part_lse[prow(lg)] : kNegInf;
+  float v0[kCombBatch][KD];
+  load_batch(0, nc0, 0, v0);
+  float m = kNegInf;
+  for (int jj = 0; jj < nc0; ++jj) m = fmaxf(m, bcast(x0, jj));
+  for (int s0 = CH; s0 < ns; s0 += CH) {
+    const int nc = ns - s0 < CH ? ns - s0 : CH;
+    const float x = (row_ok && lg < nc) ? part_lse[prow(s0 + lg)] : kNegInf;
+    for (int jj = 0; jj < nc; ++jj) m = fmaxf(m, bcast(x, jj));
   }
+  const float ms = m == kNegInf ? 0.f : m;
+  float acc[KD] = {};
+  float l = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += CH) {
+    const int nc = ns - s0 < CH ? ns - s0 : CH;
+    const float x = s0 == 0 ? x0 : ((row_ok && lg < nc) ? part_lse[prow(s0 + lg)] : kNegInf);
+    const float w = lg < nc ? fast_exp2(x - ms) : 0.f;
+    for (int j0 = 0; j0 < nc; j0 += kCombBatch) {
+      float v[kCombBatch][KD];
+      if (s0 == 0 && j0 == 0) {
+#pragma unroll
+        for (int jj = 0; jj < kCombBatch; ++jj)
+#pragma unroll
+          for (int k = 0; k < KD; ++k) v[jj][k] = v0[jj][k];
+      } else {
+        load_batch(s0, nc, j0, v);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kCombBatch; ++jj) {
+        if (j0 + jj >= nc) break;
+        const float wj = bcast(w, j0 + jj);
+        l += wj;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) acc[k] += wj * v[jj][k];
+      }
+    }
+  }
+  if (!row_ok) return;
+  const float ls = l == 0.f ? 1.f : l;
+  const int64_t orow = (int64_t)(q0 + r) * H + h;
+#pragma unroll
+  for (int k = 0; k < KD; ++k) {
+    const int d = lg + CH * k;
+    if (d < D) out[orow * D + d] = from_f<T>(acc[k] / ls);
+  }
+  if (lg == 0) lse[orow] = m == kNegInf ? kNegInf : ms + fast_log2(ls);
 }
 
 // Ordered sum of split partials (dQ): out = sum_s part[s] (partials carry the
 // softmax scale already).
 template <typename T>
-__global__ __launch_bounds__(256) void sum_combine_kernel(const float *__restrict__ part,
-                                                          T *__restrict__ out,
-                                                          const int32_t *__restrict__ items,
-                                                          int H, int D) {
-  const int item = blockIdx.x / H, h = blockIdx.x % H;
+__global__ __launch_bounds__(64 * kCombRows) void sum_combine_kernel(
+    const float *__restrict__ part, T *__restrict__ out, const int32_t *__restrict__ items, int H,
+    int D, int rblocks) {
+  constexpr int KD = kCombMaxD / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int rb = (int)blockIdx.x % rblocks, ih = (int)blockIdx.x / rblocks;
+  const int item = ih / H, h = ih - item * H;
   const PlanItem it = load_item(items, item);
   const int q0 = it.v[0], q1 = it.v[1], pbase = it.v[2], ns = it.v[3];
   const int R = q1 - q0;
-  for (int idx = threadIdx.x; idx < R * D; idx += 256) {
-    const int r = idx / D, d = idx % D;
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) acc += part[((int64_t)(pbase + s * R + r) * H + h) * D + d];
-    out[((int64_t)(q0 + r) * H + h) * D + d] = from_f<T>(acc);
+  const int r = rb * kCombRows + wave;
+  if (r >= R) return;
+  float acc[KD] = {};
+  for (int j0 = 0; j0 < ns; j0 += kCombBatch) {
+    float v[kCombBatch][KD];
+#pragma unroll
+    for (int j = 0; j < kCombBatch; ++j)
+#pragma unroll
+      for (int k = 0; k < KD; ++k) {
+        const int d = lane + 64 * k;
+        v[j][k] = (j0 + j < ns && d < D)
+                      ? part[((int64_t)(pbase + (j0 + j) * R + r) * H + h) * D + d]
+                      : 0.f;
+      }
+#pragma unroll
+    for (int j = 0; j < kCombBatch; ++j)
+#pragma unroll
+      for (int k = 0; k < KD; ++k) acc[k] += v[j][k];
+  }
+  const int64_t orow = (int64_t)(q0 + r) * H + h;
+#pragma unroll
+  for (int k = 0; k < KD; ++k) {
+    const int d = lane + 64 * k;
+    if (d < D) out[orow * D + d] = from_f<T>(acc[k]);
   }
 }
 
@@ -177,18 +274,29 @@ void launch_row_dot(const void *o, const void *dout, float *delta, int64_t rows,
 
 template <typename T>
 void launch_lse_combine(const float *part_o, const float *part_lse, void *out, float *lse,
-                        const int32_t *comb_items, int64_t n_comb, int H, int D, hipStream_t st) {
+                        const int32_t *comb_items, int64_t n_comb, int H, int D, int max_rows,
+                        hipStream_t st) {
   if (n_comb == 0) return;
-  hipLaunchKernelGGL(lse_combine_kernel<T>, dim3((unsigned)(n_comb * H)), dim3(256), 0, st,
-                     part_o, part_lse, (T *)out, lse, comb_items, H, D);
+  if (D <= 32) {
+    const int rblocks = (max_rows + 2 * kCombRows - 1) / (2 * kCombRows);
+    hipLaunchKernelGGL((lse_combine_kernel<T, 2>), dim3((unsigned)(n_comb * H * rblocks)),
+                       dim3(64 * kCombRows), 0, st, part_o, part_lse, (T *)out, lse, comb_items,
+                       H, D, rblocks);
+  } else {
+    const int rblocks = (max_rows + kCombRows - 1) / kCombRows;
+    hipLaunchKernelGGL((lse_combine_kernel<T, 1>), dim3((unsigned)(n_comb * H * rblocks)),
+                       dim3(64 * kCombRows), 0, st, part_o, part_lse, (T *)out, lse, comb_items,
+                       H, D, rblocks);
+  }
 }
 
 template <typename T>
 void launch_sum_combine(const float *part, void *out, const int32_t *comb_items, int64_t n_comb,
-                        int H, int D, hipStream_t st) {
+                        int H, int D, int max_rows, hipStream_t st) {
   if (n_comb == 0) return;
-  hipLaunchKernelGGL(sum_combine_kernel<T>, dim3((unsigned)(n_comb * H)), dim3(256), 0, st,
-                     part, (T *)out, comb_items, H, D);
+  const int rblocks = (max_rows + kCombRows - 1) / kCombRows;
+  hipLaunchKernelGGL(sum_combine_kernel<T>, dim3((unsigned)(n_comb * H * rblocks)),
+                     dim3(64 * kCombRows), 0, st, part, (T *)out, comb_items, H, D, rblocks);
 }
 
 template <typename T>
@@ -214,9 +322,9 @@ void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
   template void launch_row_dot<T>(const void *, const void *, float *, int64_t, int,        \
                                   hipStream_t);                                             \
   template void launch_lse_combine<T>(const float *, const float *, void *, float *,        \
-                                      const int32_t *, int64_t, int, int, hipStream_t);     \
+                                      const int32_t *, int64_t, int, int, int, hipStream_t);\
   template void launch_sum_combine<T>(const float *, void *, const int32_t *, int64_t, int, \
-                                      int, hipStream_t);                                    \
+                                      int, int, hipStream_t);                               \
   template void launch_absorb_dax<T>(const AbsorbArgs &, hipStream_t);                      \
   template void launch_absorb_dwv<T>(const AbsorbArgs &, hipStream_t);
 VAFA_INST(float)

@@ -31,6 +31,8 @@ FP32_CASES = [
 ]
 BF16_CASES = [FP32_CASES[i] for i in (0, 3, 4, 5, 6, 7, 8)] + [
     ("long_split", [3, 40], [5000, 9000]),
+    # more key splits (40) than one half-wave combine chunk holds (32)
+    ("many_splits", [5, 9], [40000, 300]),
     ("empty_q", [0, 5, 0], [7, 20, 0]),
 ]
 

@@ -30,6 +30,10 @@ CASES = [
     ("empty_segments", [0, 5, 9, 0], [3, 0, 40, 7], 64),
     ("long_split", [150, 20], [9000, 5000], 64),
     ("decode_split", [3, 16, 1], [3000, 1500, 1024], 128),
+    # more splits than one combine chunk holds (64 per wave row; 32 per
+    # half-wave row at D <= 32)
+    ("many_splits_d64", [20, 3], [270000, 5000], 64),
+    ("many_splits_d32", [20, 7], [140000, 900], 32),
 ]
 
 

@@ -148,8 +148,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
       }
       float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                        fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+      mx = max_xor32(max_xor16(mx)) * c;
       if (wave_any(mx > m_run + 8.0f)) {
         // lazy rescale: only when the running max grows by more than 2^8
         const float m_new = fmaxf(m_run, mx);

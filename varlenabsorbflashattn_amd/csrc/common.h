@@ -124,6 +124,25 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Max over the lane pairs (l, l^16) and (l, l^32) in registers, without the
+// LDS round trip of a shuffle: v_permlane16_swap leaves x holding rows
+// (0,0,2,2) and y rows (1,1,3,3) of the 16-lane rows of x, v_permlane32_swap
+// leaves x = (lo,lo) and y = (hi,hi) halves.  Inline asm with explicit wait
+// states around the swap (the compiler's builtin model of these swaps does
+// not track that both outputs change).
+__device__ __forceinline__ float max_xor16(float x) {
+  float y;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1"
+               : "+v"(x), "=&v"(y));
+  return fmaxf(x, y);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float y;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1"
+               : "+v"(x), "=&v"(y));
+  return fmaxf(x, y);
+}
+
 // Wave-uniform "any lane" vote.
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 

@@ -8,7 +8,8 @@
 // each tile is read from HBM/L2 once for 128 queries.  Per 64-key tile a wave
 // issues 16 MFMAs for S^T = K Q^T and 16 for O^T += V^T P^T (D=128).  The
 // online softmax runs in the log2 domain, the row max needs one cross-lane
-// exchange (lane l <-> l^32) and the row sum none until the end.
+// exchange (lane l <-> l^32, a register swap) and the row sum none until the
+// end.
 #include "kernels.h"
 #include "mfma.h"
 
@@ -135,7 +136,7 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+  mx = max_xor32(mx) * c;
   if (wave_any(mx > m_run + kLazy)) {
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2(m_run - m_new);

@@ -254,8 +254,16 @@ __global__ __launch_bounds__(256) void absorb_dwv_sum_kernel(const float *__rest
                                                              int64_t n_chunks) {
   const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (o >= n_out) return;
+  // chunk order kept; eight independent loads in flight per batch
+  constexpr int kB = 8;
   float s = 0.f;
-  for (int64_t c = 0; c < n_chunks; ++c) s += part[c * n_out + o];
+  for (int64_t c0 = 0; c0 < n_chunks; c0 += kB) {
+    float v[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) v[i] = c0 + i < n_chunks ? part[(c0 + i) * n_out + o] : 0.f;
+#pragma unroll
+    for (int i = 0; i < kB; ++i) s += v[i];
+  }
   dwv[o] = from_f<T>(s);
 }
 

@@ -131,11 +131,14 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
       for (int r = 0; r < 16; ++r)
         if (kbase + kt * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k_end) s[kt][r] = kNegInf;
   }
-  float mx = kNegInf;
+  // row max and row sum as four independent chains each: both sit on the
+  // wave's critical path between the two products
+  float m4[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+    for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], s[kt][r]);
+  float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
   mx = max_xor32(mx) * c;
   if (wave_any(mx > m_run + kLazy)) {
     const float m_new = fmaxf(m_run, mx);
@@ -147,16 +150,16 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
   }
-  float psum = 0.f;
+  float ps4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float p = fast_exp2(__builtin_fmaf(s[kt][r], c, -m_run));
       s[kt][r] = p;
-      psum += p;
+      ps4[r & 3] += p;
     }
-  l_part += psum;
+  l_part += (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
   typename M::v8 pb[2][2];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)

@@ -11,14 +11,15 @@ constexpr int kBK = 32;     // keys per LDS tile
 constexpr int kNBuf = 3;    // LDS ring depth
 constexpr int kMaxF = 256;  // D_KV handled by these kernels (padded to 32)
 
-#ifndef VAFA_ABS_XPAD
-#define VAFA_ABS_XPAD 8
-#endif
+// X rows are padded by 8 elements (stride 8*odd), which keeps the 16-byte row
+// reads conflict-free (the transposed reads then pair rows two ways; a
+// swizzled layout that removes both conflicts measured no faster).
+constexpr int kXPad = 8;
 
 template <int FP>
 struct AbsSmem {
   static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
-  static constexpr int XS = FP + VAFA_ABS_XPAD;      // padded row stride (elements)
+  static constexpr int XS = FP + kXPad;              // padded row stride (elements)
   static constexpr int kTile = kBK * XS;             // elements per tile
   static constexpr int kLoopBytes = kNBuf * kTile * 2;
   static constexpr int kEpiBytes = kAbsorbRows * XS * 2;

@@ -23,10 +23,9 @@ namespace vafa {
 namespace {
 
 constexpr int kRB = 32;  // rows per staged block (queries for dK/dV, keys for dQ)
-#ifndef VAFA_VPAD
-#define VAFA_VPAD 24
-#endif
-constexpr int kPad = VAFA_VPAD;  // LDS row padding (elements)
+// LDS row padding (elements): these tiles are read both as rows and
+// transposed; a sweep of 8/16/24/32 picked 24
+constexpr int kPad = 24;
 
 template <int D>
 struct DkvSmem {

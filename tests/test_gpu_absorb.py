@@ -140,6 +140,40 @@ def test_prepared_indices_fast_path(device):
     assert torch.equal(a, b)
 
 
+def test_prepared_indices_issue_no_device_sync(device):
+    """The prepare_target_attn_indices + validate=False contract
+    (ta/interface.py:125-138): the host cu_seqlens captured by the prepare
+    call are reused, so the inner forward + backward make no synchronizing
+    call (torch's sync debug mode turns one into an error)."""
+    q_lens, k_lens = [7, 8, 6, 9], [2048, 1024, 1536, 512]
+    q_raw, X, W_Q, W_K, W_V = (t.to(device, torch.bfloat16)
+                               for t in make_inputs(q_lens, k_lens))
+    cq, ck = cu_from_lens(q_lens).to(device), cu_from_lens(k_lens).to(device)
+    qi, ki = prepare_target_attn_indices(cq, ck)
+    from varlenabsorbflashattn_amd.absorb import _project_u
+    u = _project_u(q_raw, W_Q, W_K).contiguous()
+
+    def run():
+        uu, xx, ww = (t.detach().clone().requires_grad_(True) for t in (u, X, W_V))
+        o = target_attn_inner(uu, xx, ww, cq, ck, None, qi, ki, validate=False)
+        o.backward(torch.ones_like(o))
+        return o.detach(), uu.grad, xx.grad, ww.grad
+
+    ref = run()  # plan built and cached outside the checked region
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        got = run()
+        # control: without the prepared indices the device cu_seqlens are
+        # copied to the host, which the mode catches
+        with pytest.raises(RuntimeError):
+            target_attn_inner(u, X, W_V, cq, ck, None, validate=False)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+
+
 def test_absorb_deterministic(device):
     q_lens, k_lens = [5, 7, 9, 30], [123, 257, 999, 3000]
     outs = []

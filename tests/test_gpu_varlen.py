@@ -232,3 +232,33 @@ def test_stage1_real_shape(device):
     got, ref = run_case(q_lens, k_lens, 4, 64, torch.bfloat16, device)
     for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
         assert_close(n, a, r)
+
+
+def test_host_cu_seqlens_issue_no_device_sync(device):
+    """cu_seqlens held on the host skip the per-call device-to-host copy: the
+    plan is looked up from them directly, so a forward + backward makes no
+    synchronizing call (torch's sync debug mode turns one into an error), and
+    the results equal those of device cu_seqlens bit for bit."""
+    q, k, v, cq, ck = _inputs(device, q_lens=(300, 20, 77), k_lens=(9000, 500, 64))
+    do = torch.randn_like(q)
+    cq_h, ck_h = cq.cpu(), ck.cpu()
+
+    def run(a, b):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = packed_varlen_attn(qq, kk, vv, cu_seqlens_q=a, cu_seqlens_k=b)
+        o.backward(do)
+        return o.detach(), qq.grad, kk.grad, vv.grad
+
+    ref = run(cq, ck)
+    run(cq_h, ck_h)  # plan built and cached outside the checked region
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        got = run(cq_h, ck_h)
+        # control: device cu_seqlens are copied to the host, which the mode catches
+        with pytest.raises(RuntimeError):
+            run(cq, ck)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)

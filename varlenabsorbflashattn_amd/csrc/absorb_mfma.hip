@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   for (int i = 0; i < NF; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
-  float m_run = kNegInf, l_part = 0.f;
+  float m_run = -kHuge, l_part = 0.f;
 
   const int a_off = l16 * S::XS + lq * 8;
   const int t_off = (4 * lq + (l16 >> 2)) * S::XS + 4 * (l16 & 3);
@@ -146,11 +146,28 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
           for (int r = 0; r < 4; ++r)
             if (kb + 16 * mt + 4 * lq + r >= k1) s[mt][r] = kNegInf;
       }
-      float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-      mx = max_xor32(max_xor16(mx)) * c;
-      if (wave_any(mx > m_run + 8.0f)) {
-        // lazy rescale: only when the running max grows by more than 2^8
+      // P against the running max first; the lane's tile sum checks the
+      // bound (P <= 2^8 everywhere, or the first tile with m_run = -kHuge)
+      // and only an out-of-bound tile takes the row max and rescales.
+      v8 pb;
+      float ps;
+      auto build_p = [&]() {
+        float p2[2] = {0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = fast_exp2(__builtin_fmaf(s[mt][r], c, -m_run));
+            p2[r & 1] += p;
+            pb[4 * mt + r] = static_cast<T>(p);
+          }
+        ps = p2[0] + p2[1];
+      };
+      build_p();
+      if (wave_any(!(ps <= kLazyMax))) {
+        float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        mx = max_xor32(max_xor16(mx)) * c;
         const float m_new = fmaxf(m_run, mx);
         const float alpha = fast_exp2(m_run - m_new);
         m_run = m_new;
@@ -159,16 +176,9 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
         for (int i = 0; i < NF; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][r] *= alpha;
+        build_p();
       }
-      v8 pb;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = fast_exp2(__builtin_fmaf(s[mt][r], c, -m_run));
-          l_part += p;
-          pb[4 * mt + r] = static_cast<T>(p);
-        }
+      l_part += ps;
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ft = 0; ft < NF; ++ft) {

@@ -10,6 +10,16 @@ namespace vafa {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
 
+// Online softmax with a lazily updated running max (forward kernels): a
+// lane's P sum over one tile at or below kLazyMax (2^8) keeps the running max,
+// since every P is then below 2^8, far inside fp32 and 16-bit range.  A larger
+// sum (or an infinite one, from the initial running max -kHuge) sends the wave
+// through the path that takes the tile's row max and rescales.
+constexpr float kLazyMax = 256.0f;
+// Initial running max.  Finite, so that masked scores (-inf) still give
+// exp2(-inf) = 0 on the first tile instead of -inf + inf = NaN.
+constexpr float kHuge = 1e30f;
+
 typedef __bf16 bf16;
 typedef _Float16 f16;
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;

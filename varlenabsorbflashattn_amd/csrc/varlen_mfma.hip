@@ -7,9 +7,10 @@
 // register prefetch of the next tile, so
 // each tile is read from HBM/L2 once for 128 queries.  Per 64-key tile a wave
 // issues 16 MFMAs for S^T = K Q^T and 16 for O^T += V^T P^T (D=128).  The
-// online softmax runs in the log2 domain, the row max needs one cross-lane
-// exchange (lane l <-> l^32, a register swap) and the row sum none until the
-// end.
+// online softmax runs in the log2 domain against a lazily updated running
+// max: a tile's row max is taken (one cross-lane register swap, lane l <->
+// l^32) only when the tile's P sum shows the running max is out of date, and
+// the row sum needs no exchange until the end.
 #include "kernels.h"
 #include "mfma.h"
 
@@ -81,13 +82,25 @@ __device__ __forceinline__ void store_tile(const TileRegs<D> &r, T *ks, T *vs, i
   }
 }
 
-// Largest increase of the running row max (log2 units) absorbed without
-// rescaling the accumulators: P values stay below 2^kLazy, far inside fp32 and
-// bf16 range, and the rescale runs only when some row of the wave exceeds it.
-constexpr float kLazy = 8.0f;
+// acc + x[2t] + x[2t+1] on the dot2 unit (fp32 accumulate): the row sum of
+// P as rounded for the PV product, half the instructions of fp32 adds.
+template <typename T>
+__device__ __forceinline__ float dot2_ones(const typename Mfma<T>::v8 &x, int t, float acc);
+template <>
+__device__ __forceinline__ float dot2_ones<bf16>(const bf16x8 &x, int t, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 v = {x[2 * t], x[2 * t + 1]};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_ones<f16>(const f16x8 &x, int t, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = {x[2 * t], x[2 * t + 1]};
+  return __builtin_amdgcn_fdot2(v, __builtin_bit_cast(h2, 0x3c003c00u), acc, false);
+}
 
 // One 64-key tile for the wave's 32 query rows: S^T = K Q^T, online softmax
-// (max on raw scores, c > 0), O^T += V^T P^T.  Keys >= k_end are masked on
+// (scores scaled by c > 0), O^T += V^T P^T.  Keys >= k_end are masked on
 // the (wave-uniform) tail tile only.
 template <typename T, int D>
 __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
@@ -131,16 +144,39 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
       for (int r = 0; r < 16; ++r)
         if (kbase + kt * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k_end) s[kt][r] = kNegInf;
   }
-  // row max and row sum as four independent chains each: both sit on the
-  // wave's critical path between the two products
-  float m4[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+  // P against the running max first; the lane's sum of P as rounded to T
+  // (dot2 with (1, 1), four chains) both accumulates the row sum and checks
+  // the bound.  Only a tile whose sum exceeds kLazyMax (some P above 2^8, or
+  // the first tile, where m_run = -kHuge) takes the row max, rescales the
+  // accumulators and rebuilds P.
+  typename M::v8 pb[2][2];
+  float ps4[4];
+  auto build_p = [&]() {
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+    for (int i = 0; i < 4; ++i) ps4[i] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], s[kt][r]);
-  float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-  mx = max_xor32(mx) * c;
-  if (wave_any(mx > m_run + kLazy)) {
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        typename M::v8 x;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          x[t] = static_cast<T>(fast_exp2(__builtin_fmaf(s[kt][mm * 8 + t], c, -m_run)));
+        pb[kt][mm] = x;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ps4[t] = dot2_ones<T>(x, t, ps4[t]);
+      }
+  };
+  build_p();
+  float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+  if (wave_any(!(ps <= kLazyMax))) {
+    float m4[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], s[kt][r]);
+    float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+    mx = max_xor32(mx) * c;
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
@@ -149,22 +185,10 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
     for (int i = 0; i < ND; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+    build_p();
+    ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
   }
-  float ps4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(__builtin_fmaf(s[kt][r], c, -m_run));
-      s[kt][r] = p;
-      ps4[r & 3] += p;
-    }
-  l_part += (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-  typename M::v8 pb[2][2];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) pb[kt][mm] = pack8<T>(s[kt], mm * 8);
+  l_part += ps;
   // O^T += V^T P^T: 4*ND MFMAs ordered so consecutive ones hit different
   // accumulators, V^T operands read kPre steps ahead.
   constexpr int NP = 4 * ND;
@@ -228,7 +252,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
   for (int i = 0; i < ND; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-  float m_run = kNegInf, l_part = 0.f;
+  float m_run = -kHuge, l_part = 0.f;
 
   const int nt = (k1 - k0 + kBN - 1) / kBN;
   TileRegs<D> regs;

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
 
   auto issue = [&](int kb, int buf) {
     const int rows = k1 - kb < kBK ? (k1 - kb > 0 ? k1 - kb : 0) : kBK;
-    dma_block<FP, kDuWaves>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
+    dma_block<FP, kDuWaves, S::XS>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
                             lds_addr(smem + buf * S::kTile), wave, lane);
   };
 #pragma unroll
@@ -193,7 +193,7 @@ constexpr int kDxWaves = 4;
 
 template <int FP>
 struct DxSmem {
-  static constexpr int XS = AbsSmem<FP>::XS;
+  static constexpr int XS = AbsSmem<FP, kXPad32>::XS;  // 32-row operand reads
   static constexpr int kBlk = 32 * XS;                    // one [32][XS] row block
   static constexpr int kBufBytes = 2 * kBlk * 2 + 2 * 32 * 4;  // U, dAX, LSE, delta
   static constexpr int kBytes = 2 * kBufBytes;
@@ -243,8 +243,8 @@ struct DxItem {
     const int rb = r0 + blk * 32;
     const int rows = r1 - rb < 32 ? r1 - rb : 32;
     const int64_t nb = (int64_t)rows * F * 2;
-    dma_block<FP, kDxWaves>(u + (int64_t)rb * F, nb, F, lds_addr(base), wave, lane);
-    dma_block<FP, kDxWaves>(dax + (int64_t)rb * F, nb, F, lds_addr(base + S::kBlk * 2), wave,
+    dma_block<FP, kDxWaves, XS>(u + (int64_t)rb * F, nb, F, lds_addr(base), wave, lane);
+    dma_block<FP, kDxWaves, XS>(dax + (int64_t)rb * F, nb, F, lds_addr(base + S::kBlk * 2), wave,
                             lane);
     const float *vec = (wave & 1) ? delta : lse;
     const u32x4 rv = rsrc_words(vec + rb, (int64_t)rows * 4);

@@ -11,15 +11,19 @@ constexpr int kBK = 32;     // keys per LDS tile
 constexpr int kNBuf = 3;    // LDS ring depth
 constexpr int kMaxF = 256;  // D_KV handled by these kernels (padded to 32)
 
-// X rows are padded by 8 elements (stride 8*odd), which keeps the 16-byte row
-// reads conflict-free (the transposed reads then pair rows two ways; a
-// swizzled layout that removes both conflicts measured no faster).
-constexpr int kXPad = 8;
+// Row padding of the staged tiles (elements), by operand read pattern,
+// measured on gfx950 at 12 waves per CU with FP = 256: the 16x16x32 kernels
+// read 16 rows x 4 chunks (ds_read_b128) and 16x16 transposed operands
+// (ds_read_b64_tr_b16), both fastest at a stride of 16*odd elements (FP + 16:
+// 29 and 17 cycles per read against 52 and 29 at FP + 8); the 32x32x16
+// kernels read 32 rows x 2 chunks, fastest at 8*odd (FP + 8: 29 against 52).
+constexpr int kXPad16 = 16;
+constexpr int kXPad32 = 8;
 
-template <int FP>
+template <int FP, int Pad = kXPad16>
 struct AbsSmem {
   static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
-  static constexpr int XS = FP + kXPad;              // padded row stride (elements)
+  static constexpr int XS = FP + Pad;                // padded row stride (elements)
   static constexpr int kTile = kBK * XS;             // elements per tile
   static constexpr int kLoopBytes = kNBuf * kTile * 2;
   static constexpr int kEpiBytes = kAbsorbRows * XS * 2;
@@ -46,10 +50,9 @@ struct Mfma16<f16> {
 // zeros); each of the workgroup's NW waves moves 32/NW rows, one instruction
 // per row.  The descriptor is rebased per row in scalar registers, so the
 // only per-lane operand is the chunk offset.
-template <int FP, int NW>
+template <int FP, int NW, int XS>
 __device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
                                           int wave, int lane) {
-  constexpr int XS = AbsSmem<FP>::XS;
   const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
   if (lane < FP / 8) {
 #pragma unroll

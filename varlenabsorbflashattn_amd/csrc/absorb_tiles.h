@@ -48,19 +48,23 @@ struct Mfma16<f16> {
 // LDS-DMA of 32 consecutive rows [F] of a row slab (src, bytes) into a
 // padded [32][XS] LDS block (rows past the slab and chunks past F arrive as
 // zeros); each of the workgroup's NW waves moves 32/NW rows, one instruction
-// per row.  The descriptor is rebased per row in scalar registers, so the
-// only per-lane operand is the chunk offset.
+// per row.  One descriptor covers the block's valid bytes and the row offset
+// sits in the lane offset (the range check covers the lane offset, not
+// soffset), added by one volatile VALU add per row so that the compiler does
+// not hoist the rows' offsets into separate registers.  Chunks past F carry an
+// offset of 2^31 and read as zeros.
 template <int FP, int NW, int XS>
 __device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
                                           int wave, int lane) {
+  const u32x4 rs = rsrc_words(src, bytes);
   const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
   if (lane < FP / 8) {
 #pragma unroll
     for (int n = 0; n < 32 / NW; ++n) {
       const int r = wave * (32 / NW) + n;
-      const int64_t ro = (int64_t)r * F * 2;
-      lds_dma16(rsrc_words(static_cast<const char *>(src) + ro, bytes - ro), base + r * XS * 2,
-                (int32_t)off);
+      int32_t voff;
+      asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(r * F * 2), "v"(off));
+      lds_dma16(rs, base + r * XS * 2, voff);
     }
   }
 }

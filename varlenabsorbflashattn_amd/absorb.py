@@ -208,16 +208,56 @@ def target_attn_inner(
         q_chunk_indices, k_chunk_indices, validate)
 
 
+class _HeadProject(torch.autograd.Function):
+    """u[t,h,:] = q_proj[t,h,:] W_K[:,h,:]^T for every head (the einsum of
+    ta/interface.py:435).
+
+    Forward: ONE GEMM of q_proj ``[T, H*D_H]`` against the block-diagonal
+    ``[H*D_H, H*d_kv]`` matrix of the W_K[:,h,:]^T blocks, which writes u
+    token-major ``[T, H, d_kv]`` directly -- no per-head outputs and no
+    stacking copy (the stack was a full extra read + write of u).  For finite
+    q_proj the zero blocks add exact zeros to each fp32 sum, so every u
+    element is the same sum of products as per head (an infinite q_proj
+    element would spread NaN to the other heads' columns through 0 * inf).
+    Backward: per head on strided views (plain
+    2-D GEMMs, no batched products), so the zero blocks cost nothing there:
+    dq_proj[:,h,:] = du[:,h,:] W_K[:,h,:],  dW_K[:,h,:] = du[:,h,:]^T q_proj[:,h,:].
+    """
+
+    @staticmethod
+    def forward(ctx, q_proj: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
+        d_kv, H, _ = W_K.shape
+        blocks = torch.block_diag(*[W_K[:, h, :].t() for h in range(H)])
+        ctx.save_for_backward(q_proj, W_K)
+        return (q_proj @ blocks).view(q_proj.shape[0], H, d_kv)
+
+    @staticmethod
+    def backward(ctx, du: torch.Tensor):
+        q_proj, W_K = ctx.saved_tensors
+        d_kv, H, D_H = W_K.shape
+        du2 = du.reshape(du.shape[0], H * d_kv)
+        dq = torch.empty_like(q_proj) if ctx.needs_input_grad[0] else None
+        dW = torch.empty_like(W_K) if ctx.needs_input_grad[1] else None
+        for h in range(H):
+            du_h = du2[:, h * d_kv:(h + 1) * d_kv]
+            if dq is not None:
+                dq[:, h * D_H:(h + 1) * D_H] = du_h @ W_K[:, h, :]
+            if dW is not None:
+                dW[:, h, :] = du_h.t() @ q_proj[:, h * D_H:(h + 1) * D_H]
+        return dq, dW
+
+
 def _project_u(q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
     """u[t,h,:] = (q_raw[t] W_Q[:,h,:]) W_K[:,h,:]^T (ta/interface.py:434-435).
 
-    One 2-D GEMM for all heads of W_Q, then one 2-D GEMM per head for W_K
-    (no batched products; same per-element math as the reference einsum).
+    One 2-D GEMM for all heads of W_Q (rounded to the input dtype, as the
+    reference's q projection is), then ``_HeadProject`` for W_K: u comes out
+    contiguous ``[T_q, H, d_kv]``.
     """
     T_q, d_q = q_raw.shape
     _, H, D_H = W_Q.shape
-    q_proj = (q_raw @ W_Q.reshape(d_q, H * D_H)).view(T_q, H, D_H)
-    return torch.stack([q_proj[:, h, :] @ W_K[:, h, :].t() for h in range(H)], dim=1)
+    q_proj = q_raw @ W_Q.reshape(d_q, H * D_H)
+    return _HeadProject.apply(q_proj, W_K)
 
 
 def packed_target_attn(

@@ -188,12 +188,15 @@ def bench_varlen_c3(iters):
     return case, ms
 
 
-def bench_absorb(case, iters, d_q=None):
+def bench_absorb(case, iters, d_q=None, full=False):
     """Inner absorb forward on precomputed u, through the reference's hot-path
     contract: prepare_target_attn_indices once, then validate=False calls
-    (ta/interface.py:125-138) -- no host round trip inside the timed loop."""
+    (ta/interface.py:125-138) -- no host round trip inside the timed loop.
+    With ``full``, also times the whole packed_target_attn forward (u
+    projection included) on the same inputs; returns (inner ms, full ms)."""
     import torch
-    from varlenabsorbflashattn_amd import prepare_target_attn_indices, target_attn_inner
+    from varlenabsorbflashattn_amd import (packed_target_attn, prepare_target_attn_indices,
+                                           target_attn_inner)
     from varlenabsorbflashattn_amd import workloads as W
     from varlenabsorbflashattn_amd.absorb import _project_u
     dev = torch.device("cuda:0")
@@ -210,9 +213,19 @@ def bench_absorb(case, iters, d_q=None):
 
     fwd()
     ms = time_region(fwd, iters)
+    full_ms = None
+    if full:
+        def full_fwd():
+            with torch.no_grad():
+                packed_target_attn(q_raw, X, W_Q, W_K, W_V, cu_seqlens_q=cq, cu_seqlens_k=ck,
+                                   q_chunk_indices=qi, k_chunk_indices=ki, scale=scale,
+                                   validate=False)
+
+        full_fwd()
+        full_ms = time_region(full_fwd, iters)
     del q_raw, X, u
     torch.cuda.empty_cache()
-    return ms
+    return (ms, full_ms) if full else ms
 
 
 def bench_absorb_bwd(case, iters, d_q=None):
@@ -363,11 +376,12 @@ def main():
             "TFLOP/s": c3.flops_fwd / (c3_ms * 1e-3) / 1e12}
         log("C3", secondary["c3_varlen_splitk_fwd"])
         for cfg in (W.config4(seed=0), W.config5(seed=0)):
-            a_ms = bench_absorb(cfg, max(3, args.steps // 2))
+            a_ms, full_ms = bench_absorb(cfg, max(3, args.steps // 2), full=True)
             gbs = cfg.bytes_fwd() / (a_ms * 1e-3) / 1e9
             secondary[cfg.name + "_fwd"] = {
                 "ms": a_ms, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
                 "TFLOP/s": cfg.flops_fwd / (a_ms * 1e-3) / 1e12,
+                "packed_target_attn_ms": full_ms,
                 "sum_lq": int(sum(cfg.q_lens)), "sum_lk": int(sum(cfg.k_lens))}
             log(cfg.name, secondary[cfg.name + "_fwd"])
         c4 = W.config4(seed=0)

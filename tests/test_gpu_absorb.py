@@ -85,6 +85,20 @@ def test_absorb_bf16_parity(device, name, q_lens, k_lens):
         assert_close(n, a, r)
 
 
+# head counts and head dims off the benchmark shape (rows of a workgroup are
+# laid out head-major, 64 / H tokens per head)
+HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 216)]
+
+
+@pytest.mark.parametrize("H,D_H,d_kv", HEAD_SHAPES, ids=[f"H{h}_DH{d}_F{f}" for h, d, f in HEAD_SHAPES])
+def test_absorb_bf16_head_shapes(device, H, D_H, d_kv):
+    print(f"[absorb bf16 heads] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
+    q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
+    got, ref = run_case(q_lens, k_lens, torch.bfloat16, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)
+    for n, a, r in zip(NAMES, got, ref):
+        assert_close(n, a, r)
+
+
 def test_absorb_bf16_config4_dims(device):
     """C4 dims (D_in=256, N(0,1) inputs, Xavier weights) on a small sample."""
     from varlenabsorbflashattn_amd import workloads as W

@@ -2,16 +2,18 @@
 // (replaces ta/kernels.py:185-284, the default "alpha" forward).
 //
 // One workgroup = 4 waves x 16 rows owns up to 64 (token, head) rows of one
-// sample -- all H heads of 64/H consecutive tokens, token-major, so the rows
-// are one contiguous slab of u -- and one key range.  Raw X is streamed once
-// per workgroup (not once per head) through a 3-deep ring of 32-key LDS tiles
+// sample -- all H heads of 64/H consecutive tokens, one contiguous slab of u
+// -- and one key range.  Raw X is streamed once per workgroup (not once per
+// head) through a 3-deep ring of 32-key LDS tiles
 // filled by buffer_load ... lds, one instruction per padded row (no staging
 // registers; rows past the key range arrive as zeros).  Per tile each wave
 // issues S^T = X U^T (X rows as the A operand) and aX^T += X^T P^T (X^T from
 // ds_read_b64_tr_b16) as 16x16x32 products, LDS operands read a few products
-// ahead, with the online softmax in the log2 domain.  After the key loop aX/l
-// is rounded to the input dtype, regrouped head-major in LDS and projected by
-// W_V (16x16x32 products).
+// ahead, with the online softmax in the log2 domain.  The workgroup's rows
+// are head-major (a wave's 16 rows span at most two heads), so after the key
+// loop each wave rounds aX/l to the input dtype in registers and projects it
+// by its heads' W_V (16x16x32 products, W_V^T stored in the accumulators'
+// f order): no LDS staging and no barrier in the epilogue.
 #include "absorb_tiles.h"
 
 namespace vafa {
@@ -21,8 +23,11 @@ namespace {
 using namespace absorb;
 
 
-// W_V [F, H, DH] -> wvt [H, DH, FP] (zero-padded over f), the B-operand
-// layout of the projection (8 consecutive f per lane).
+// W_V [F, H, DH] -> wvt [H, DH, FP] (zero-padded over f): the A operand of
+// the projection O^T = W_V^T (aX/l)^T.  Within each 32-wide f chunk,
+// position 8a + b holds f = 4a + b (b < 4) or 16 + 4a + b - 4 (b >= 4), the
+// order in which the forward's accumulators present aX^T (rows 4a..4a+3 of
+// the chunk's two 16-row tiles).
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__ wv,
                                                            T *__restrict__ wvt, int H, int F,
@@ -30,9 +35,11 @@ __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__
   const int64_t n = (int64_t)H * DH * FP;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const int f = (int)(i % FP);
+  const int p = (int)(i % FP);
   const int d = (int)((i / FP) % DH);
   const int h = (int)(i / ((int64_t)FP * DH));
+  const int a = (p & 31) >> 3, b = p & 7;
+  const int f = (p & ~31) + (b < 4 ? 4 * a + b : 16 + 4 * a + b - 4);
   wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
 }
 
@@ -59,10 +66,16 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
-  const int nrows = (t1 - t0) * H;
-  const int row = wave * 16 + l16;  // local (token-major) row
-  const bool row_ok = row < nrows;
-  const bool wave_active = wave * 16 < nrows;
+  // Rows are head-major inside the workgroup: row r is token r % TT of head
+  // r / TT (TT = 64 / H tokens), so a wave's 16 rows span at most two heads
+  // and the W_V projection runs on the accumulators in registers.
+  const int ntok = t1 - t0;
+  const int nrows = ntok * H;
+  const int TT = kAbsorbRows / H;
+  const int row = wave * 16 + l16;
+  const int tl = row % TT, hh = row / TT;  // token / head of this lane's row
+  const bool row_ok = tl < ntok;
+  const bool wave_active = (wave * 16) % TT < ntok;
   const int nt = (k1 - k0 + kBK - 1) / kBK;
 
   auto issue = [&](int kb, int buf) {
@@ -83,7 +96,8 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) {
       const int ch = kc * 4 + lq;
-      u32x4 w = buf_load16(ru, ch < fchunks ? row * F * 2 + ch * 16 : 0x7fffffff);
+      // rows past the item's tokens lie past the descriptor's range: zeros
+      u32x4 w = buf_load16(ru, ch < fchunks ? (tl * H + hh) * F * 2 + ch * 16 : 0x7fffffff);
       // waited for here, in the prologue, not inside the key loop where a
       // compiler vmcnt wait would also drain the LDS-DMA ring
       asm volatile("" : "+v"(w));
@@ -190,73 +204,65 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
     buf = buf == kNBuf - 1 ? 0 : buf + 1;
   }
   wait_vmcnt<0>();
-  __syncthreads();
 
-  // ---- epilogue: aX/l -> LDS (head-major rows, input dtype), then W_V ----
+  // ---- epilogue: O = round(aX / l) W_V from the accumulators ----
+  // The four lanes of a column hold its P-sum partials.
   float l = l_part + __shfl_xor(l_part, 16, 64);
   l += __shfl_xor(l, 32, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int TT = kAbsorbRows / H;         // tokens per workgroup
-  const int tl = row / H, hh = row % H;   // token / head of this lane's row
   if (row_ok && lq == 0) {
     const float lse_v = l > 0.f ? m_run + fast_log2(l) : kNegInf;
     if (pbase < 0)
-      lse[(int64_t)t0 * H + row] = lse_v;
+      lse[(int64_t)(t0 + tl) * H + hh] = lse_v;
     else
       part_lse[(int64_t)(pbase + tl) * H + hh] = lse_v;
   }
-  T *axs = smem;  // [kAbsorbRows][XS], row h*TT + t
-  if (wave_active) {
-    typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-    T *dst = axs + (hh * TT + tl) * S::XS + lq * 4;
+  if (!wave_active) return;
+  // B operand of O^T = W_V^T (aX/l)^T for 32-wide f chunk kc: k slot t of
+  // lane group lq is f = 32*kc + 4*lq + t (t < 4, from acc[2kc]) or
+  // 32*kc + 16 + 4*lq + t - 4 (t >= 4, from acc[2kc+1]); wvt stores W_V^T in
+  // that order, so the A operand is one 16-byte load.
+  v8 bx[NK];
 #pragma unroll
-    for (int ft = 0; ft < NF; ++ft) {
-      T4 w;
+  for (int kc = 0; kc < NK; ++kc)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(row_ok ? acc[ft][e] * inv : 0.f);
-      *reinterpret_cast<T4 *>(dst + ft * 16) = w;
-    }
-  }
-  __syncthreads();
-  // projection: per (head, 16-token tile, 16-wide d tile) one 16x16 output;
-  // the tile's W_V operands are all requested before the first product
-  const int ntok = t1 - t0;
-  const int tiles_per_head = (TT + 15) / 16;
-  const int n_tiles = H * tiles_per_head * (DH / 16);
-  for (int tile = wave; tile < n_tiles; tile += kFwdWaves) {
-    const int dtile = tile % (DH / 16);
-    const int tt = (tile / (DH / 16)) % tiles_per_head;
-    const int h = tile / ((DH / 16) * tiles_per_head);
-    if (tt * 16 >= ntok) continue;
-    const T *arow = axs + (h * TT + tt * 16 + l16) * S::XS + lq * 8;
-    const T *brow = wvt + ((int64_t)h * DH + dtile * 16 + l16) * FP + lq * 8;
-    const bool a_ok = tt * 16 + l16 < TT;
-    u32x4 bw[NK];
+    for (int t = 0; t < 8; ++t)
+      bx[kc][t] = static_cast<T>(acc[2 * kc + (t >> 2)][t & 3] * inv);
+  const int h_first = (wave * 16) / TT;
+  const int nh = TT >= 16 ? 1 : 16 / TT;  // heads among the wave's rows
+  constexpr int ND16 = DH / 16;
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
+  for (int hx = 0; hx < nh; ++hx) {
+    const int h = h_first + hx;
+    const T *arow = wvt + ((int64_t)h * DH + l16) * FP + lq * 8;
 #pragma unroll
-    for (int kc = 0; kc < NK; ++kc) bw[kc] = *reinterpret_cast<const u32x4 *>(brow + kc * 32);
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < ND16; ++dt) {
+      u32x4 wa[NK];
 #pragma unroll
-    for (int kc = 0; kc < NK; ++kc) {
-      const u32x4 a = a_ok ? *reinterpret_cast<const u32x4 *>(arow + kc * 32)
-                           : u32x4{0u, 0u, 0u, 0u};
-      o = M16::mma(as_v8<T>(a), as_v8<T>(bw[kc]), o);
-    }
+      for (int kc = 0; kc < NK; ++kc)
+        wa[kc] = *reinterpret_cast<const u32x4 *>(arow + dt * 16 * FP + kc * 32);
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = tt * 16 + lq * 4 + r;
-      if (tok >= ntok) continue;
-      const int d = dtile * 16 + l16;
-      if (pbase < 0)
-        O[((int64_t)(t0 + tok) * H + h) * DH + d] = static_cast<T>(o[r]);
-      else
-        part_o[((int64_t)(pbase + tok) * H + h) * DH + d] = o[r];
+      for (int kc = 0; kc < NK; ++kc) o = M16::mma(as_v8<T>(wa[kc]), bx[kc], o);
+      // lane: row l16 (token tl of head hh), d = 16*dt + 4*lq + r
+      if (row_ok && hh == h) {
+        const int d = dt * 16 + lq * 4;
+        if (pbase < 0) {
+          T4 w;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[r] = static_cast<T>(o[r]);
+          *reinterpret_cast<T4 *>(O + ((int64_t)(t0 + tl) * H + hh) * DH + d) = w;
+        } else {
+          *reinterpret_cast<f32x4 *>(part_o + ((int64_t)(pbase + tl) * H + hh) * DH + d) = o;
+        }
+      }
     }
   }
 }
 
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
-  const int smem = AbsSmem<FP>::kBytes;
+  const int smem = AbsSmem<FP>::kLoopBytes;
   hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(64 * kFwdWaves),

@@ -159,26 +159,34 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     typename M::v8 tring[kPre];
 #pragma unroll
     for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+    // P = exp2(S*c - LSE) and dS = P (dP - delta) per accumulator row r
+    // (query 8*(r/4) + 4*lhalf + r%4 of the block); keys past k1 have zero K
+    // and V rows, their dK / dV columns are never stored, so their P needs no
+    // masking.
+    typename M::v8 pb[2], sb[2];
+    // rows 0..7 (first 16 queries) before the products; rows 8..15 are
+    // computed under the first half of the chain, which only reads rows 0..7,
+    // their LSE / delta read one product ahead
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 2; ++g) {
       const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
       const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = g * 4 + e;
-        // keys past k1 have zero K and V rows; their dK / dV columns are
-        // never stored, so their P needs no masking
         const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
         s[r] = p;
         dp[r] = p * (dp[r] - Dl[e]);
       }
     }
-    typename M::v8 pb[2], sb[2];
+    pb[0] = pack8<T>(s, 0);
+    sb[0] = pack8<T>(dp, 0);
+    constexpr int kRowsPer = 8 / (2 * ND);  // second-half rows per first-half product
+    auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
+    auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
+    float Ln[kRowsPer], Dn[kRowsPer];
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      pb[mm] = pack8<T>(s, mm * 8);
-      sb[mm] = pack8<T>(dp, mm * 8);
-    }
+    for (int rr = 0; rr < kRowsPer; ++rr) Ln[rr] = lse_at(8 + rr), Dn[rr] = del_at(8 + rr);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4 * ND; ++i) {
@@ -189,6 +197,29 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
       else
         adv[dt] = M::mma(a, pb[mm], adv[dt]);
       if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
+      if (i < 2 * ND) {
+        float Lc[kRowsPer], Dc[kRowsPer];
+#pragma unroll
+        for (int rr = 0; rr < kRowsPer; ++rr) {
+          Lc[rr] = Ln[rr], Dc[rr] = Dn[rr];
+          if (i + 1 < 2 * ND) {
+            const int rn = 8 + (i + 1) * kRowsPer + rr;
+            Ln[rr] = lse_at(rn);
+            Dn[rr] = del_at(rn);
+          }
+        }
+#pragma unroll
+        for (int rr = 0; rr < kRowsPer; ++rr) {
+          const int r = 8 + i * kRowsPer + rr;
+          const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lc[rr]));
+          s[r] = p;
+          dp[r] = p * (dp[r] - Dc[rr]);
+        }
+        if (i == 2 * ND - 1) {
+          pb[1] = pack8<T>(s, 8);
+          sb[1] = pack8<T>(dp, 8);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }

@@ -242,3 +242,15 @@ def test_plan_rejects_bad_cu():
         _lib.plan_varlen(np.array([0, 5, 3]), np.array([0, 1, 2]), 2, 64)
     with pytest.raises(AssertionError):
         _lib.plan_varlen(np.array([0, 5]), np.array([0, 1, 2]), 2, 64)
+
+
+def test_host_cu_pair_matches_single_copies():
+    import torch
+    from varlenabsorbflashattn_amd import _lib
+    a = torch.tensor([0, 3, 7, 7, 12], dtype=torch.int32)
+    b = torch.tensor([0, 5, 9, 20, 21], dtype=torch.int32)
+    for x, y in ((a, a), (a, b), (a, b.to(torch.int64)), (a.numpy(), b)):
+        hx, hy = _lib.as_host_i64_pair(x, y)
+        assert hx.dtype == np.int64 and hy.dtype == np.int64
+        assert np.array_equal(hx, _lib.as_host_i64(x))
+        assert np.array_equal(hy, _lib.as_host_i64(y))

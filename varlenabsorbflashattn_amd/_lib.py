@@ -10,7 +10,7 @@ import ctypes as C
 import os
 import threading
 from collections import OrderedDict
-from typing import Optional
+from typing import Optional, Tuple
 
 import numpy as np
 
@@ -129,6 +129,22 @@ def as_host_i64(x) -> np.ndarray:
     except ImportError:  # pragma: no cover
         pass
     return np.ascontiguousarray(np.asarray(x, dtype=np.int64))
+
+
+def as_host_i64_pair(a, b) -> Tuple[np.ndarray, np.ndarray]:
+    """Host int64 copies of two cu_seqlens tensors with one device sync: the
+    same tensor is copied once, two device tensors of one shape and dtype are
+    stacked on the device and copied together."""
+    import torch
+    if a is b:
+        h = as_host_i64(a)
+        return h, h
+    if (isinstance(a, torch.Tensor) and isinstance(b, torch.Tensor) and a.is_cuda and b.is_cuda
+            and a.device == b.device and a.dtype == b.dtype and a.shape == b.shape
+            and a.dim() == 1):
+        h = as_host_i64(torch.stack((a.detach(), b.detach())))
+        return np.ascontiguousarray(h[0]), np.ascontiguousarray(h[1])
+    return as_host_i64(a), as_host_i64(b)
 
 
 # ---- host metadata -----------------------------------------------------------

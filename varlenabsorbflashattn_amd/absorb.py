@@ -90,8 +90,7 @@ def prepare_target_attn_indices(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.
     Passing them back with ``validate=False`` skips every host round trip:
     the host cu_seqlens captured here are reused to look up the cached plan.
     """
-    cu_q_h = _lib.as_host_i64(cu_seqlens_q)
-    cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+    cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
     q_idx = torch.from_numpy(_lib.chunk_indices(cu_q_h, _BT_Q_FWD)).to(cu_seqlens_q.device)
     k_idx = torch.from_numpy(_lib.chunk_indices(cu_k_h, _BT_K_BWD)).to(cu_seqlens_k.device)
     _remember_host_cu(q_idx, cu_q_h, cu_k_h)
@@ -129,8 +128,7 @@ class _TargetAttnFunction(torch.autograd.Function):
         if known is not None and not validate:
             cu_q_h, cu_k_h = known
         else:
-            cu_q_h = _lib.as_host_i64(cu_seqlens_q)
-            cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+            cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
         if validate:
             n_seg = cu_seqlens_q.numel() - 1
             assert cu_seqlens_k.numel() - 1 == n_seg, "segment count mismatch q vs k"

@@ -101,8 +101,14 @@ class _PackedVarlenAttnFunction(torch.autograd.Function):
         n_seg = cu_seqlens_q.numel() - 1
         assert cu_seqlens_k.numel() - 1 == n_seg, \
             f"segment count mismatch: q has {n_seg}, k has {cu_seqlens_k.numel()-1}"
-        cu_q_h = _lib.as_host_i64(cu_seqlens_q)
-        cu_k_h = _lib.as_host_i64(cu_seqlens_k)
+        # work that does not need the host copy of cu_seqlens goes first: the
+        # copy waits for the GPU work already queued, and what follows it runs
+        # while the GPU is idle
+        q, k, v = _aligned(q), _aligned(k), _aligned(v)
+        o = torch.empty_like(q)
+        lse = torch.empty((T_q, H), dtype=torch.float32, device=q.device)
+        L = _lib.lib()
+        cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
         _validate_cu_seqlens(cu_q_h, cu_seqlens_q.shape, T_q, "cu_seqlens_q")
         _validate_cu_seqlens(cu_k_h, cu_seqlens_k.shape, T_k, "cu_seqlens_k")
         if cu_q_h.ndim != 1 or cu_q_h.size < 2:
@@ -110,10 +116,6 @@ class _PackedVarlenAttnFunction(torch.autograd.Function):
 
         plan = _lib.device_plan("varlen", cu_q_h, cu_k_h, (H, D), q.device)
         _check_tokens(plan.info, T_q, T_k)
-        q, k, v = _aligned(q), _aligned(k), _aligned(v)
-        o = torch.empty_like(q)
-        lse = torch.empty((T_q, H), dtype=torch.float32, device=q.device)
-        L = _lib.lib()
         ws = _workspace(L.vafa_varlen_fwd_workspace(plan.info, D), q.device)
         _lib.check(L.vafa_varlen_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),

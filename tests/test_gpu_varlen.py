@@ -201,11 +201,13 @@ def test_multi_seed(device, seed):
         assert_close(n, a, r)
 
 
-def test_backward_stages_match_fused(device):
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_backward_stages_match_fused(device, D):
     """vafa_varlen_bwd_stage (delta, dQ, dK/dV launched separately) reproduces
-    vafa_varlen_bwd bit for bit."""
+    vafa_varlen_bwd, whose dQ kernel forms delta itself, bit for bit."""
     from varlenabsorbflashattn_amd.varlen import BackwardStages
-    q, k, v, cq, ck = _inputs(device, q_lens=(300, 20, 77), k_lens=(9000, 500, 64), D=128)
+    print(f"[varlen stages] D={D}", flush=True)
+    q, k, v, cq, ck = _inputs(device, q_lens=(300, 20, 77), k_lens=(9000, 500, 64), D=D)
     do = torch.randn_like(q)
     qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
     o = packed_varlen_attn(qq, kk, vv, cu_seqlens_q=cq, cu_seqlens_k=ck)

@@ -115,11 +115,16 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
   }
 }
 
+// All stages in order.  The matrix-core dQ kernel forms delta itself (the
+// same bits as the delta stage) and leaves it for dK/dV.
 template <typename T>
 void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
-  varlen_bwd_stage<T>(VAFA_BWD_DELTA, a, st);
-  varlen_bwd_stage<T>(VAFA_BWD_DQ, a, st);
-  varlen_bwd_stage<T>(VAFA_BWD_DKV, a, st);
+  const bool mfma = sizeof(T) == 2 && (a.D == 32 || a.D == 64 || a.D == 128);
+  VarlenArgs f = a;
+  f.fuse_delta = mfma;
+  if (!mfma) varlen_bwd_stage<T>(VAFA_BWD_DELTA, f, st);
+  varlen_bwd_stage<T>(VAFA_BWD_DQ, f, st);
+  varlen_bwd_stage<T>(VAFA_BWD_DKV, f, st);
 }
 
 // ---- absorb ---------------------------------------------------------------

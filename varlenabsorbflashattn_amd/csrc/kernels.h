@@ -21,6 +21,9 @@ struct VarlenArgs {
   int H, D;
   float scale;
   int stage;  // backward stage (VAFA_BWD_*) or -1 for all
+  // the matrix-core dQ kernel computes delta from O and dO itself and writes
+  // it for dK/dV (no separate row_dot launch)
+  bool fuse_delta;
 };
 
 struct AbsorbArgs {

@@ -9,8 +9,10 @@ namespace vafa {
 namespace {
 
 // delta[r] = sum_d o[r,d] * dout[r,d] in fp32 (fa/kernels.py:186-216,
-// ta/kernels.py:298-325).  Each thread reads one 16-byte chunk of a row; the
-// D/CH threads of a row reduce with lane shuffles, so loads are coalesced.
+// ta/kernels.py:298-325).  Each thread reads one 16-byte chunk of a row and
+// sums it by fused multiply-adds in element order; the D/CH threads of a row
+// reduce with a lane butterfly, so loads are coalesced.  The varlen dQ kernel
+// reproduces this order when it forms delta itself.
 template <typename T>
 __global__ __launch_bounds__(256) void row_dot_kernel(const T *__restrict__ o,
                                                       const T *__restrict__ dout,
@@ -28,7 +30,7 @@ __global__ __launch_bounds__(256) void row_dot_kernel(const T *__restrict__ o,
     const T *x = reinterpret_cast<const T *>(&a);
     const T *y = reinterpret_cast<const T *>(&b);
 #pragma unroll
-    for (int e = 0; e < CH; ++e) s += to_f(x[e]) * to_f(y[e]);
+    for (int e = 0; e < CH; ++e) s = __builtin_fmaf(to_f(x[e]), to_f(y[e]), s);
   }
   for (int off = tpr >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
   if (r < rows && part == 0) delta[r] = s;

@@ -290,9 +290,9 @@ struct DqSmem {
 template <typename T, int D>
 __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
-    const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
-    T *__restrict__ dq, float *__restrict__ part_dq, const int32_t *__restrict__ items, int H,
-    float c, float scale) {
+    const T *__restrict__ dout, const float *__restrict__ lse, float *delta,
+    const T *__restrict__ o_fused, T *__restrict__ dq, float *__restrict__ part_dq,
+    const int32_t *__restrict__ items, int H, float c, float scale) {
   using M = Mfma<T>;
   using S = DqSmem<D>;
   constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
@@ -326,11 +326,19 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   if (nblk > 0) load_rows<T, D, 128>(stg, src, k0, k1, H, h, st);
 
   typename M::v8 qf[NC], dof[NC];
+  // O rows for delta (fused mode), requested with Q and dO: one round trip
+  const bool fused = o_fused != nullptr;
+  u32x4 ov[NC];
   {
     const int64_t nb = (int64_t)(q1 - q0) * H * D * 2;
     const rsrc_t rq = make_rsrc(q + (int64_t)q0 * H * D, nb);
     const rsrc_t rd = make_rsrc(dout + (int64_t)q0 * H * D, nb);
     const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
+    if (fused) {
+      const rsrc_t ro = make_rsrc(o_fused + (int64_t)q0 * H * D, nb);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) ov[cc] = buf_load16(ro, off + cc * 32);
+    }
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
       u32x4 a = buf_load16(rq, off + cc * 32), b = buf_load16(rd, off + cc * 32);
@@ -340,7 +348,31 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     }
   }
   float Lr = row_ok ? lse[(int64_t)qrow * H + h] : __builtin_inff();
-  float Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+  float Dr;
+  if (fused) {
+    // delta = rowsum(O * dO) from the dO operands and the O rows read in the
+    // same layout, summed in row_dot_kernel's order (per 16-byte chunk
+    // sequentially, then a butterfly over the chunks; this lane holds chunks
+    // 2*cc + lhalf) so both produce the same bits.  The item that owns the
+    // rows' first key range writes it for dK/dV.
+    float sc[NC];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const T *x = reinterpret_cast<const T *>(&ov[cc]);
+      float acc_c = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc_c = __builtin_fmaf(to_f(x[e]), to_f(dof[cc][e]), acc_c);
+      sc[cc] = acc_c;
+    }
+#pragma unroll
+    for (int half = NC / 2; half >= 1; half /= 2)
+#pragma unroll
+      for (int cc = 0; cc < half; ++cc) sc[cc] = sc[cc] + sc[cc + half];
+    Dr = sc[0] + __shfl_xor(sc[0], 32, 64);
+    if (row_ok && lhalf == 0 && it.v[6] == 0) delta[(int64_t)qrow * H + h] = Dr;
+  } else {
+    Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+  }
   asm volatile("" : "+v"(Lr), "+v"(Dr));
   f32x16 acc[ND];
 #pragma unroll
@@ -461,8 +493,9 @@ void launch_mfma_varlen_dq(const VarlenArgs &a, hipStream_t st) {
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   hipLaunchKernelGGL((varlen_dq_kernel<T, D>), dim3((unsigned)(a.n_items * a.H)), dim3(256),
                      smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
-                     (const T *)a.dout, a.lse_in, a.delta, (T *)a.dq, a.part_o, a.items, a.H,
-                     a.scale * kLog2e, a.scale);
+                     (const T *)a.dout, a.lse_in, a.delta,
+                     a.fuse_delta ? (const T *)a.o_in : nullptr, (T *)a.dq, a.part_o, a.items,
+                     a.H, a.scale * kLog2e, a.scale);
 }
 
 #define VAFA_INST(T, D)                                                           \

@@ -210,3 +210,23 @@ def test_absorb_validation_errors(device):
     with pytest.raises(ValueError):
         packed_target_attn(*ins, cu_seqlens_q=torch.tensor([0, 2, 6], device=device),
                            cu_seqlens_k=torch.tensor([0, 4, 9], device=device))
+
+
+def test_absorb_bf16_flag_3d_inputs_and_seqinfo(device):
+    """packed_target_attn's input forms (ta/interface.py:357-445): bf16=True on
+    fp32 inputs, [1, T, d] inputs and seqinfo lengths all give the output of
+    the plain call on bf16 inputs with cu_seqlens, bit for bit."""
+    q_lens, k_lens = [3, 8, 1], [50, 700, 9]
+    ins = make_inputs(q_lens, k_lens)
+    cq, ck = cu_from_lens(q_lens).to(device), cu_from_lens(k_lens).to(device)
+    b16 = [t.to(torch.bfloat16).to(device) for t in ins]
+    base = packed_target_attn(*b16, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    flag = packed_target_attn(*(t.to(device) for t in ins), cu_seqlens_q=cq, cu_seqlens_k=ck,
+                              bf16=True)
+    assert flag.dtype == torch.bfloat16 and torch.equal(flag, base)
+    three = packed_target_attn(b16[0].unsqueeze(0), b16[1].unsqueeze(0), *b16[2:],
+                               cu_seqlens_q=cq, cu_seqlens_k=ck)
+    assert torch.equal(three, base)
+    seqinfo = packed_target_attn(*b16, q_seqinfo=torch.tensor(q_lens, device=device),
+                                 k_seqinfo=torch.tensor(k_lens, device=device))
+    assert torch.equal(seqinfo, base)

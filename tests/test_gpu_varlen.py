@@ -264,3 +264,88 @@ def test_host_cu_seqlens_issue_no_device_sync(device):
         torch.cuda.set_sync_debug_mode(0)
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+def test_noncontiguous_inputs_match_contiguous(device):
+    """Non-contiguous q/k/v views (the stress option of
+    fa-tools/benchmark_packed_varlen_flash_attn.py:248-253) give the results of
+    their contiguous copies bit for bit, and the grads reach the views' bases."""
+    q, k, v, cq, ck = _inputs(device, q_lens=(70, 130), k_lens=(90, 300), D=64)
+    do = torch.randn_like(q)
+    T, H, D = q.shape
+    qb = torch.zeros(T, H, 2 * D, device=device, dtype=q.dtype)
+    qb[..., ::2] = q                                   # stride(-1) == 2
+    kb = k.transpose(0, 1).contiguous()                # view strides (D, T*D, 1)
+    vb = torch.cat([v, torch.zeros_like(v)], dim=1)    # view strides (2*H*D, D, 1)
+    for t in (qb, kb, vb):
+        t.requires_grad_(True)
+    views = (qb[..., ::2], kb.transpose(0, 1), vb[:, :H])
+    assert not any(t.is_contiguous() for t in views)
+    o1 = packed_varlen_attn(*views, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    o1.backward(do)
+    q2, k2, v2 = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o2 = packed_varlen_attn(q2, k2, v2, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    o2.backward(do)
+    assert torch.equal(o1, o2)
+    assert torch.equal(qb.grad[..., ::2], q2.grad) and not qb.grad[..., 1::2].any()
+    assert torch.equal(kb.grad.transpose(0, 1), k2.grad)
+    assert torch.equal(vb.grad[:, :H], v2.grad) and not vb.grad[:, H:].any()
+
+
+def _gpu_errors(out, ref):
+    """The parity.py metric evaluated on the GPU (for tensors too large to
+    move to the host): max of |out - ref| minus the rounding of ref to the
+    output dtype, and mean |out - ref|, both divided by max(1, rms(ref))."""
+    a, r = out.detach().float(), ref.detach().float()
+    floor = (r.to(out.dtype).float() - r).abs()
+    s = max(1.0, r.pow(2).mean().sqrt().item())
+    d = (a - r).abs()
+    return (d - floor).max().item() / s, d.mean().item() / s
+
+
+def test_varlen_business_scale(device):
+    """fa/test_smoke.py:666-767: 50 segments x Q=500 against K_total = 2M keys
+    with pareto-distributed key lengths (H=4, D=64, bf16), forward and grads
+    against a float32 torch reference computed per segment on the GPU."""
+    n, Lq, H, D, K_total = 50, 500, 4, 64, 2_000_000
+    rng = np.random.default_rng(0)
+    w = rng.pareto(1.5, n) + 1.0
+    k_lens = np.maximum(1, np.floor(w / w.sum() * K_total)).astype(np.int64)
+    k_lens[0] += K_total - int(k_lens.sum())
+    q_lens = [Lq] * n
+    print(f"[varlen business] n={n} Lq={Lq} K_total={int(k_lens.sum())} max_k={int(k_lens.max())}",
+          flush=True)
+    g = torch.Generator(device=device).manual_seed(0)
+    Tq, Tk = n * Lq, int(k_lens.sum())
+    q = torch.randn(Tq, H, D, device=device, generator=g).to(torch.bfloat16)
+    k = torch.randn(Tk, H, D, device=device, generator=g).to(torch.bfloat16)
+    v = torch.randn(Tk, H, D, device=device, generator=g).to(torch.bfloat16)
+    do = torch.randn(Tq, H, D, device=device, generator=g).to(torch.bfloat16)
+    cq, ck = cu_from_lens(q_lens).to(device), cu_from_lens(k_lens.tolist()).to(device)
+    qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = packed_varlen_attn(qd, kd, vd, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    o.backward(do)
+    scale = 1.0 / math.sqrt(D)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    o_r = torch.empty(Tq, H, D, device=device)
+    dq_r = torch.empty(Tq, H, D, device=device)
+    dk_r = torch.empty(Tk, H, D, device=device)
+    dv_r = torch.empty(Tk, H, D, device=device)
+    q0 = k0 = 0
+    for lk in k_lens.tolist():
+        qs, ks, vs = (t.float().transpose(0, 1).contiguous().requires_grad_(True)
+                      for t in (q[q0:q0 + Lq], k[k0:k0 + lk], v[k0:k0 + lk]))
+        p = torch.softmax(torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale, dim=-1)
+        os_ = torch.matmul(p, vs)
+        os_.backward(do[q0:q0 + Lq].float().transpose(0, 1).contiguous())
+        o_r[q0:q0 + Lq] = os_.detach().transpose(0, 1)
+        dq_r[q0:q0 + Lq] = qs.grad.transpose(0, 1)
+        dk_r[k0:k0 + lk] = ks.grad.transpose(0, 1)
+        dv_r[k0:k0 + lk] = vs.grad.transpose(0, 1)
+        q0 += Lq
+        k0 += lk
+    for name, a, r in (("o", o, o_r), ("dq", qd.grad, dq_r), ("dk", kd.grad, dk_r),
+                       ("dv", vd.grad, dv_r)):
+        mx, mn = _gpu_errors(a, r)
+        print(f"  {name:8s} max_excess={mx:.3e} mean_abs={mn:.3e}")
+        assert mx <= 2e-2 and mn <= 2e-3, f"{name}: max {mx:.3e} mean {mn:.3e}"

@@ -131,7 +131,9 @@ VAFA_API int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *
                     void *stream);
 
 /* Replaces _PackedVarlenAttnFunction.backward (fa/interface.py:252-341):
- * dO [T_q,H,D] -> dq, dk, dv (same dtype as q). Deterministic (no atomics). */
+ * dO [T_q,H,D] -> dq, dk, dv (same dtype as q). Deterministic (no atomics).
+ * Runs the stages below in order; on the matrix-core path the dQ stage forms
+ * delta itself (bit-identical to stage 0) and leaves it for dK/dV. */
 VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
                     const void *dout, const float *lse, void *dq, void *dk, void *dv,
                     const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,

@@ -254,3 +254,25 @@ def test_host_cu_pair_matches_single_copies():
         assert hx.dtype == np.int64 and hy.dtype == np.int64
         assert np.array_equal(hx, _lib.as_host_i64(x))
         assert np.array_equal(hy, _lib.as_host_i64(y))
+
+
+def test_absorb_split_chunk_follows_total_work():
+    """Key ranges split only beyond a chunk that grows with the launch's total
+    work: thousands of samples of <= 8192 keys (configs[3] / configs[4]
+    shapes) stay whole, while a handful of very long samples are split into
+    chunks of at least 1024 keys so that they fill the GPU."""
+    from varlenabsorbflashattn_amd import workloads as W
+
+    def split_counts(ql, kl):
+        p = check_absorb_plan(ql, kl)
+        fwd = [r for r in p.section("fwd").tolist() if r[5] >= 0]
+        return len(fwd), int(p.info.max_split), fwd
+
+    for cfg in (W.config4(seed=0), W.config5(seed=0, n=2048)):
+        n, ms, _ = split_counts(cfg.q_lens, cfg.k_lens)
+        assert ms == 1, cfg.name
+    n, ms, fwd = split_counts([8] * 10, [100000] * 10)
+    assert ms > 16 and n == 10 * ms
+    assert min(k1 - k0 for _, _, k0, k1, *_ in fwd) >= 1024 - 64
+    _, ms, _ = split_counts([5, 9], [40000, 300])
+    assert ms == 40  # the many-splits GPU case keeps its 40 chunks

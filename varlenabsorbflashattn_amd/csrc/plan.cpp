@@ -317,9 +317,22 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   if (H < 1) return fail(VAFA_ERR_ASSERT, "H must be >= 1");
   (void)D_KV;
   (void)D_H;
-  const SplitPolicy &pol = kAbsorbPolicy;
   const int64_t TT = std::max<int64_t>(1, kAbsorbRows / H);
   const int64_t BK = kAbsorbKTile;
+  // Key chunk of split segments, from the launch's total work: a chunk holds
+  // kAbsorbSplitSlack times the average keys per resident forward workgroup
+  // (never below kAbsorbPolicy.long_chunk), and only longer key ranges split.
+  // Longest-first order starts such items at once, so they end within the
+  // kernel; every extra item costs a prologue, an epilogue and a combine.
+  SplitPolicy pol = kAbsorbPolicy;
+  {
+    int64_t work = 0;  // sum over segments of (token tiles x keys)
+    for (int64_t s = 0; s + 1 < n1; ++s)
+      if (cu_q[s + 1] > cu_q[s]) work += cdiv(cu_q[s + 1] - cu_q[s], TT) * (cu_k[s + 1] - cu_k[s]);
+    const int64_t chunk = round_up(cdiv(kAbsorbSplitSlack * work, kAbsorbSlots), pol.align);
+    pol.long_chunk = std::max<int64_t>(pol.long_chunk, chunk);
+    pol.long_threshold = pol.long_chunk;
+  }
   std::memset(info, 0, sizeof(*info));
   info->magic = VAFA_PLAN_MAGIC;
   info->kind = 2;

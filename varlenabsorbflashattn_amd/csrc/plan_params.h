@@ -26,7 +26,16 @@ struct SplitPolicy {
 };
 
 constexpr SplitPolicy kVarlenPolicy{16, 1024, 2048, 4, 16, 4096, 4096, 64, 64};
-constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 2048, 1024, 64, 32};
+// Absorb: long_chunk is the smallest key chunk; the planner raises chunk and
+// threshold with the launch's total work (see vafa_plan_absorb).
+constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 1024, 1024, 64, 32};
+// Resident absorb forward workgroups on the MI355X (256 CUs x 3), and the
+// multiple of the average keys per workgroup that a key range may hold
+// before it is split (measured: splitting configs[4]'s <= 8192-key samples
+// into 1024-key chunks cost 10%, configs[3]'s <= 2000-key samples at 1024
+// keys 4%).
+constexpr int64_t kAbsorbSlots = 768;
+constexpr int64_t kAbsorbSplitSlack = 3;
 
 // Workgroups are dispatched round-robin over this many XCDs (one L2 each):
 // workgroup i runs on XCD i % kXcds.

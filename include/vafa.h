@@ -179,6 +179,16 @@ VAFA_API int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, cons
                     int64_t D_H, int32_t dtype, float scale, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
+/* The head projection of packed_target_attn, which the reference runs as a
+ * torch einsum (ta/interface.py:434-435, 'thd,khd->thk'):
+ * u[t,h,f] = sum_d q_proj[t, h*D_H + d] * W_K[f,h,d] with q_proj [T_q, H*D_H],
+ * W_K [D_KV,H,D_H] -> u [T_q,H,D_KV], all in the given 16-bit dtype (fp32
+ * accumulation, one rounding).  D_KV a multiple of 8, D_H a multiple of 16
+ * up to 128; other shapes and fp32 return VAFA_ERR_VALUE. */
+VAFA_API int vafa_absorb_project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q,
+                                   int64_t H, int64_t D_KV, int64_t D_H, int32_t dtype,
+                                   void *stream);
+
 #ifdef __cplusplus
 }
 #endif

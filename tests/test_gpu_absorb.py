@@ -231,3 +231,22 @@ def test_absorb_bf16_flag_3d_inputs_and_seqinfo(device):
     seqinfo = packed_target_attn(*b16, q_seqinfo=torch.tensor(q_lens, device=device),
                                  k_seqinfo=torch.tensor(k_lens, device=device))
     assert torch.equal(seqinfo, base)
+
+
+@pytest.mark.parametrize("T,d_kv,H,D_H", [(9424, 256, 8, 32), (37, 216, 8, 32), (100, 64, 2, 16),
+                                          (70, 192, 4, 128), (5, 128, 1, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_project_u_kernel(device, T, d_kv, H, D_H, dtype):
+    """vafa_absorb_project_u (the head einsum of ta/interface.py:435 on matrix
+    cores) against a float64 einsum of the same 16-bit inputs: within one
+    rounding to the output dtype, token-major [T, H, d_kv] layout."""
+    from varlenabsorbflashattn_amd.absorb import _HeadProject
+    g = torch.Generator().manual_seed(T + d_kv)
+    q_proj = torch.randn(T, H * D_H, generator=g).to(dtype)
+    W_K = (torch.randn(d_kv, H, D_H, generator=g) * 0.2).to(dtype)
+    u = _HeadProject.apply(q_proj.to(device), W_K.to(device)).cpu()
+    ref = torch.einsum("thk,jhk->thj", q_proj.double().view(T, H, D_H), W_K.double())
+    assert u.shape == (T, H, d_kv) and u.dtype == dtype
+    err = (u.double() - ref).abs()
+    bound = ref.abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-6
+    assert (err <= bound).all(), float((err - bound).max())

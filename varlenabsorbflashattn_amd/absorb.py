@@ -210,11 +210,12 @@ class _HeadProject(torch.autograd.Function):
     """u[t,h,:] = q_proj[t,h,:] W_K[:,h,:]^T for every head (the einsum of
     ta/interface.py:435).
 
-    Forward: ONE GEMM of q_proj ``[T, H*D_H]`` against the block-diagonal
-    ``[H*D_H, H*d_kv]`` matrix of the W_K[:,h,:]^T blocks, which writes u
-    token-major ``[T, H, d_kv]`` directly -- no per-head outputs and no
-    stacking copy (the stack was a full extra read + write of u).  For finite
-    q_proj the zero blocks add exact zeros to each fp32 sum, so every u
+    Forward: for 16-bit inputs, ``vafa_absorb_project_u`` (per-head products
+    on matrix cores, u written token-major ``[T, H, d_kv]``, fp32 sums rounded
+    once).  Otherwise ONE GEMM of q_proj ``[T, H*D_H]`` against the
+    block-diagonal ``[H*D_H, H*d_kv]`` matrix of the W_K[:,h,:]^T blocks, which
+    also writes u token-major -- no per-head outputs and no stacking copy.  For
+    finite q_proj the zero blocks add exact zeros to each fp32 sum, so every u
     element is the same sum of products as per head (an infinite q_proj
     element would spread NaN to the other heads' columns through 0 * inf).
     Backward: per head on strided views (plain
@@ -224,9 +225,20 @@ class _HeadProject(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q_proj: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
-        d_kv, H, _ = W_K.shape
-        blocks = torch.block_diag(*[W_K[:, h, :].t() for h in range(H)])
+        d_kv, H, D_H = W_K.shape
         ctx.save_for_backward(q_proj, W_K)
+        if (q_proj.is_cuda and q_proj.dtype in (torch.bfloat16, torch.float16)
+                and W_K.dtype == q_proj.dtype and d_kv % 8 == 0 and D_H % 16 == 0
+                and D_H <= 128):
+            # matrix-core kernel: per-head products written token-major
+            qp = _aligned(q_proj.contiguous())
+            wk = _aligned(W_K.contiguous())
+            u = torch.empty((q_proj.shape[0], H, d_kv), dtype=q_proj.dtype, device=q_proj.device)
+            _lib.check(_lib.lib().vafa_absorb_project_u(
+                qp.data_ptr(), wk.data_ptr(), u.data_ptr(), q_proj.shape[0], H, d_kv, D_H,
+                _lib.dtype_code(q_proj.dtype), _lib.stream_ptr(q_proj.device)))
+            return u
+        blocks = torch.block_diag(*[W_K[:, h, :].t() for h in range(H)])
         return (q_proj @ blocks).view(q_proj.shape[0], H, d_kv)
 
     @staticmethod

@@ -343,6 +343,28 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   return check_launch("vafa_absorb_fwd");
 }
 
+int vafa_absorb_project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q, int64_t H,
+                          int64_t D_KV, int64_t D_H, int32_t dtype, void *stream) {
+  if (T_q < 0 || H < 1 || H > 1024)
+    return fail(VAFA_ERR_VALUE, "project_u: bad T_q=%lld / H=%lld", (long long)T_q, (long long)H);
+  if (!absorb_project_supported((int)D_KV, (int)D_H))
+    return fail(VAFA_ERR_VALUE, "project_u: D_KV=%lld (multiple of 8) / D_H=%lld "
+                "(multiple of 16, <= 128) not supported", (long long)D_KV, (long long)D_H);
+  switch (dtype) {
+    case VAFA_BF16:
+      launch_absorb_project_u<bf16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H,
+                                    (hipStream_t)stream);
+      break;
+    case VAFA_F16:
+      launch_absorb_project_u<f16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H,
+                                   (hipStream_t)stream);
+      break;
+    default:
+      return fail(VAFA_ERR_VALUE, "project_u: 16-bit dtypes only (got %d)", (int)dtype);
+  }
+  return check_launch("vafa_absorb_project_u");
+}
+
 int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O,
                     const void *dO, const float *lse, void *du, void *dX, void *dW_V,
                     const int32_t *plan_dev, const vafa_plan_info *info, int64_t D_KV,

@@ -85,6 +85,10 @@ template <typename T, int D> void launch_mfma_varlen_dkv(const VarlenArgs &, hip
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
+bool absorb_project_supported(int F, int DH);
+template <typename T>
+void launch_absorb_project_u(const void *q_proj, const void *wk, void *u, int64_t T_q, int H,
+                             int F, int DH, hipStream_t st);
 // absorb_bwd_mfma.hip: du/aX (query side) and dX (key side) on matrix cores
 template <typename T> void launch_mfma_absorb_du(const AbsorbArgs &, hipStream_t);
 // dAX = dO W_V^T; false (nothing launched) for a D_H it does not cover

@@ -3,6 +3,7 @@
 // Every reduction runs in a fixed order, so results are bit-reproducible.
 #include "common.h"
 #include "kernels.h"
+#include "plan_params.h"
 
 namespace vafa {
 
@@ -207,12 +208,23 @@ __global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ d
 // dW_V^T[d, f] += dO^T[d, t] aX[t, f] two tokens per product, lane l feeding
 // token t + l/32 at d (A) and f (B) = l % 32.
 template <typename T>
+__device__ __forceinline__ float bits_to_f(uint32_t b) {
+  if constexpr (std::is_same<T, float>::value) return __uint_as_float(b);
+  else if constexpr (std::is_same<T, bf16>::value) return __uint_as_float(b << 16);
+  else return (float)__builtin_bit_cast(f16, (uint16_t)b);
+}
+
+template <typename T>
 __global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
     const float *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
-    int64_t T_q, int64_t tchunk, int H, int F, int DH) {
+    int64_t T_q, int64_t tchunk, int H, int F, int DH, int n_waves) {
   const int lane = threadIdx.x, l32 = lane & 31, kt = lane >> 5;
   const int nfs = (F + 31) / 32, nds = (DH + 31) / 32;
+  // workgroup i runs on XCD i % kXcds: give each XCD a contiguous run of
+  // waves, so the F/32 waves that read the same dO rows share one L2
   int w = blockIdx.x;
+  w = (w % kXcds) * (int)(gridDim.x / kXcds) + w / kXcds;
+  if (w >= n_waves) return;
   const int ds = w % nds;
   w /= nds;
   const int fs = w % nfs;
@@ -226,17 +238,42 @@ __global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.f;
   constexpr int kU = 8;  // token pairs per batch of loads
-  for (int64_t t = ta; t < tb; t += 2 * kU) {
-    float av[kU], bv[kU];
+  // Branch-free loads: every lane reads a clamped, in-range element and the
+  // select to zero comes after all loads are issued, so a batch is one round
+  // trip (predicated loads compile to branches that wait on each load).
+  const int dc = d_ok ? d : DH - 1, fc = f_ok ? f : F - 1;
+  auto load = [&](int64_t t, float(&av)[kU], float(&bv)[kU]) {
+    // dO bits go into separate 32-bit registers: 16-bit elements loaded as T
+    // get packed two per register, and each load then waits on the previous
+    using Bits = typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type;
+    uint32_t ra[kU];
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
-      const int64_t tt = t + 2 * i + kt;
-      const bool ok = tt < tb;
-      av[i] = ok && d_ok ? to_f(dO[(tt * H + h) * DH + d]) : 0.f;
-      bv[i] = ok && f_ok ? ax[(tt * H + h) * F + f] : 0.f;
+      const int64_t tt = t + 2 * i + kt, tc = tt < tb ? tt : tb - 1;
+      ra[i] = reinterpret_cast<const Bits *>(dO)[(tc * H + h) * DH + dc];
+      bv[i] = ax[(tc * H + h) * F + fc];
     }
 #pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      const bool ok = t + 2 * i + kt < tb;
+      av[i] = ok && d_ok ? bits_to_f<T>(ra[i]) : 0.f;
+      bv[i] = ok && f_ok ? bv[i] : 0.f;
+    }
+  };
+  auto product = [&](const float(&av)[kU], const float(&bv)[kU]) {
+#pragma unroll
     for (int i = 0; i < kU; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[i], acc, 0, 0, 0);
+  };
+  // two register batches: the next batch's loads are in flight while the
+  // matrix cores consume the current one
+  float a0[kU], b0[kU], a1[kU], b1[kU];
+  load(ta, a0, b0);
+  for (int64_t t = ta; t < tb; t += 4 * kU) {
+    load(t + 2 * kU, a1, b1);
+    product(a0, b0);
+    if (t + 2 * kU >= tb) break;
+    load(t + 4 * kU, a0, b0);
+    product(a1, b1);
   }
   // acc element r: d = ds*32 + (r/4)*8 + kt*4 + r%4, f = this lane's f
   if (!f_ok) return;
@@ -321,8 +358,9 @@ void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
   const int64_t n_out = (int64_t)a.F * a.H * a.DH;
   if (a.n_tchunks > 0) {
     const int64_t waves = a.n_tchunks * a.H * ((a.F + 31) / 32) * ((a.DH + 31) / 32);
-    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3((unsigned)waves), dim3(64), 0, st, a.ax,
-                       (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH);
+    const int64_t grid = (waves + kXcds - 1) / kXcds * kXcds;
+    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3((unsigned)grid), dim3(64), 0, st, a.ax,
+                       (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH, (int)waves);
   }
   hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st,
                      a.dwv_part, (T *)a.dwv, n_out, a.n_tchunks);

@@ -99,6 +99,8 @@ typedef struct vafa_plan_info {
   int64_t q_tile, k_tile;         /* tile sizes the plan was built for     */
   int64_t max_split;              /* largest number of splits of one tile  */
   int64_t max_comb_rows;          /* most rows (tokens) of one combine item */
+  int64_t n_kv_res;               /* absorb: the leading key-tile items whose
+                                     segment has at most 64 (token, head) rows */
 } vafa_plan_info;
 
 /* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).

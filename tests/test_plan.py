@@ -276,3 +276,25 @@ def test_absorb_split_chunk_follows_total_work():
     assert min(k1 - k0 for _, _, k0, k1, *_ in fwd) >= 1024 - 64
     _, ms, _ = split_counts([5, 9], [40000, 300])
     assert ms == 40  # the many-splits GPU case keeps its 40 chunks
+
+
+def test_absorb_kv_resident_items_lead():
+    """The key-chunk section lists segments with at most 64 (token, head) rows
+    first, n_kv_res of them, so the resident-row and streamed dX kernels are
+    each launched over only their own items; order within each run is still
+    longest-first."""
+    H = 8
+    q_lens = [1, 8, 9, 0, 20, 3, 8, 100, 2, 9]
+    k_lens = [500, 3000, 40, 7, 9000, 1, 260, 129, 64, 5000]
+    p = check_absorb_plan(q_lens, k_lens, H=H)
+    kv = p.section("kv").tolist()
+    n_res = int(p.info.n_kv_res)
+    assert len(kv) == int(p.info.n_kv) and 0 < n_res < len(kv)
+    rows = [(q1 - q0) * H for (_, _, q0, q1, *_) in kv]
+    assert all(r <= 64 for r in rows[:n_res]) and all(r > 64 for r in rows[n_res:])
+    up = lambda x, m: (x + m - 1) // m * m
+    for run in (kv[:n_res], kv[n_res:]):
+        cost = [up(k1 - k0, 128) * up((q1 - q0) * H, 32) for (k0, k1, q0, q1, *_) in run]
+        assert cost == sorted(cost, reverse=True)
+    # varlen plans have no such split
+    assert int(_lib.plan_varlen(_cu([5, 7]), _cu([5, 7]), 2, 64).info.n_kv_res) == 0

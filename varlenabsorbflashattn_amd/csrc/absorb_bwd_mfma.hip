@@ -426,7 +426,7 @@ __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_res_kernel(
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const D d(u, X, dax, lse, delta, smem_raw, load_item(items, blockIdx.x), H, F);
   const int nblk = d.nblk();
-  if (nblk > 2) return;  // streamed by absorb_dx_kernel
+  if (nblk * 32 > kDxResidentRows) return;  // streamed by absorb_dx_kernel
   const int nsub = d.nsub();
   if (nblk == 0) {
     // a sample without queries: its keys get zero gradient
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_kernel(
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const D d(u, X, dax, lse, delta, smem_raw, load_item(items, blockIdx.x), H, F);
   const int nblk = d.nblk();
-  if (nblk <= 2) return;  // resident items: absorb_dx_res_kernel
+  if (nblk * 32 <= kDxResidentRows) return;  // resident items: absorb_dx_res_kernel
   const int nsub = d.nsub();
   v8 xf[D::NC];
   d.issue(0, 0);
@@ -580,17 +580,25 @@ void launch_du_fp(const AbsorbArgs &a, hipStream_t st) {
 template <typename T, int FP>
 void launch_dx_fp(const AbsorbArgs &a, hipStream_t st) {
   const int smem = DxSmem<FP>::kBytes;
-  // both kernels walk the whole key-chunk section; each skips the other's items
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_res_kernel<T, FP>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((absorb_dx_res_kernel<T, FP>), dim3((unsigned)a.n_kv), dim3(64 * kDxWaves),
-                     smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
-                     a.delta, (T *)a.dX, a.kv_items, a.H, a.F, a.scale * kLog2e, a.scale);
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)a.n_kv), dim3(64 * kDxWaves),
-                     smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
-                     a.delta, (T *)a.dX, a.kv_items, a.H, a.F, a.scale * kLog2e, a.scale);
+  // the plan puts the resident-row items first (items are 8 int32 each): each
+  // kernel gets its own run of the key-chunk section and still skips any item
+  // of the other kind
+  const int64_t n_res = a.n_kv_res, n_str = a.n_kv - a.n_kv_res;
+  if (n_res > 0) {
+    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_res_kernel<T, FP>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    hipLaunchKernelGGL((absorb_dx_res_kernel<T, FP>), dim3((unsigned)n_res), dim3(64 * kDxWaves),
+                       smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
+                       a.delta, (T *)a.dX, a.kv_items, a.H, a.F, a.scale * kLog2e, a.scale);
+  }
+  if (n_str > 0) {
+    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)n_str), dim3(64 * kDxWaves),
+                       smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
+                       a.delta, (T *)a.dX, a.kv_items + n_res * 8, a.H, a.F,
+                       a.scale * kLog2e, a.scale);
+  }
 }
 
 }  // namespace

@@ -33,6 +33,8 @@ struct Carver {
 int check_info(const vafa_plan_info *info, int64_t kind) {
   if (info == nullptr || info->magic != VAFA_PLAN_MAGIC || info->kind != kind)
     return fail(VAFA_ERR_VALUE, "plan does not belong to this operator");
+  if (info->n_kv_res < 0 || info->n_kv_res > info->n_kv)
+    return fail(VAFA_ERR_VALUE, "plan info is inconsistent (n_kv_res)");
   return VAFA_OK;
 }
 
@@ -335,7 +337,7 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.comb_rows = (int)info->max_comb_rows;
-  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv; a.n_kv_res = info->n_kv_res;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;
   a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
@@ -384,7 +386,7 @@ int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.comb_rows = (int)info->max_comb_rows;
-  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
+  a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv; a.n_kv_res = info->n_kv_res;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;
   a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;

@@ -39,6 +39,7 @@ struct AbsorbArgs {
   void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
   const int32_t *items, *comb_items, *kv_items, *qseg_items;
   int64_t n_items, n_comb, n_kv, n_qseg;
+  int64_t n_kv_res;           // leading kv items for absorb_dx_res_kernel
   int comb_rows;              // most tokens of one combine item
   int64_t T_q, T_k;
   int64_t n_tchunks, tchunk;

@@ -387,6 +387,11 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   }
   fwd = xcd_bundle(fwd);
   sort_lpt(kv);
+  // resident-row items first, so each dX kernel is launched over its own items
+  const auto res_end = std::stable_partition(kv.begin(), kv.end(), [H](const Item &it) {
+    return (int64_t)(it.v[3] - it.v[2]) * H <= kDxResidentRows;
+  });
+  info->n_kv_res = (int64_t)(res_end - kv.begin());
   sort_lpt(qt);
   info->n_part_rows = prow;
   info->max_split = max_split;

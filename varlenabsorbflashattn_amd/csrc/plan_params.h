@@ -41,4 +41,9 @@ constexpr int64_t kAbsorbSplitSlack = 3;
 // workgroup i runs on XCD i % kXcds.
 constexpr int kXcds = 8;
 
+// Absorb dX: a segment with at most this many (token, head) rows keeps all of
+// them resident in one workgroup (absorb_dx_res_kernel); longer segments are
+// streamed in 32-row blocks (absorb_dx_kernel).
+constexpr int kDxResidentRows = 64;
+
 }  // namespace vafa

@@ -536,7 +536,8 @@ template <typename T, int DH>
 __global__ __launch_bounds__(64) void absorb_dax_kernel(const T *__restrict__ dO,
                                                         const T *__restrict__ wv,
                                                         T *__restrict__ dax, int64_t T_q, int H,
-                                                        int F) {
+                                                        int F, const T *__restrict__ O,
+                                                        float *__restrict__ delta) {
   using M = Mfma<T>;
   constexpr int KC = DH / 16;
   const int lane = threadIdx.x, l32 = lane & 31, lh = lane >> 5;
@@ -552,6 +553,21 @@ __global__ __launch_bounds__(64) void absorb_dax_kernel(const T *__restrict__ dO
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc)
     a[kc] = as_v8<T>(buf_load16(rd, ((l32 * H + h) * DH + kc * 16 + lh * 8) * 2));
+  if (fg == 0) {
+    // delta[t,h] = sum_d dO[t,h,d] O[t,h,d] (ta/kernels.py:298-325) from the
+    // dO rows already in registers; each half-wave holds half of every row
+    const rsrc_t ro = make_rsrc(O + t0 * H * DH, (int64_t)nt * H * DH * 2);
+    float sd = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const typename M::v8 ov =
+          as_v8<T>(buf_load16(ro, ((l32 * H + h) * DH + kc * 16 + lh * 8) * 2));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sd = __builtin_fmaf(to_f(a[kc][e]), to_f(ov[e]), sd);
+    }
+    sd += __shfl_xor(sd, 32, 64);
+    if (lane < 32 && l32 < nt) delta[(t0 + l32) * H + h] = sd;
+  }
   // the wave's [32 tokens, kDaxTiles*32 f] block is staged in LDS, then
   // written as contiguous row runs (16 bytes per lane when F % 8 == 0)
   constexpr int kW = kDaxTiles * 32;
@@ -654,10 +670,10 @@ bool launch_mfma_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
   const unsigned grid =
       (unsigned)(((a.T_q + 31) / 32) * a.H * ((((a.F + 31) / 32) + kDaxTiles - 1) / kDaxTiles));
   switch (a.DH) {
-    case 16: hipLaunchKernelGGL((absorb_dax_kernel<T, 16>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
-    case 32: hipLaunchKernelGGL((absorb_dax_kernel<T, 32>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
-    case 64: hipLaunchKernelGGL((absorb_dax_kernel<T, 64>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
-    case 128: hipLaunchKernelGGL((absorb_dax_kernel<T, 128>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F); return true;
+    case 16: hipLaunchKernelGGL((absorb_dax_kernel<T, 16>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
+    case 32: hipLaunchKernelGGL((absorb_dax_kernel<T, 32>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
+    case 64: hipLaunchKernelGGL((absorb_dax_kernel<T, 64>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
+    case 128: hipLaunchKernelGGL((absorb_dax_kernel<T, 128>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
     default: return false;
   }
 }

@@ -177,12 +177,15 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
 
 template <typename T>
 void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
-  launch_row_dot<T>(a.O_in, a.dO, a.delta, a.T_q * a.H, a.DH, st);
   bool mfma = false;
   if constexpr (sizeof(T) == 2) mfma = mfma_absorb_supported<T>(a.H, a.F, a.DH);
+  // the matrix-core dAX kernel also writes delta (sum_d dO O) for its rows
   bool dax_done = false;
   if constexpr (sizeof(T) == 2) dax_done = launch_mfma_absorb_dax<T>(a, st);
-  if (!dax_done) launch_absorb_dax<T>(a, st);
+  if (!dax_done) {
+    launch_row_dot<T>(a.O_in, a.dO, a.delta, a.T_q * a.H, a.DH, st);
+    launch_absorb_dax<T>(a, st);
+  }
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
       launch_mfma_absorb_du<T>(a, st);

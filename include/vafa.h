@@ -55,10 +55,15 @@ VAFA_API const char *vafa_last_error(void);
  * length or a total above INT32_MAX. */
 VAFA_API int vafa_seqinfo_to_cu(const int64_t *seqinfo, int64_t n, int32_t *cu_out);
 
-/* Replaces fa/interface.py:96-118 and ta/interface.py:92-106
- * (_validate_cu_seqlens): n1 >= 2, cu[0]==0, cu[n1-1]==T, non-decreasing.
+/* Replaces fa/interface.py:96-118 (_validate_cu_seqlens of the varlen
+ * operator): n1 >= 2, cu[0]==0, cu[n1-1]==T, non-decreasing.
  * `name` is used in the error message. */
 VAFA_API int vafa_validate_cu(const int64_t *cu, int64_t n1, int64_t T, const char *name);
+
+/* Replaces ta/interface.py:92-106 (_validate_cu_seqlens of the absorb
+ * operator): the same checks in the same order, with that operator's error
+ * texts ("<name>[0] must be 0", "<name> must be non-decreasing", ...). */
+VAFA_API int vafa_validate_cu_absorb(const int64_t *cu, int64_t n1, int64_t T, const char *name);
 
 /* Replaces ta/interface.py:109-116 (_validate_active_segments_have_keys). */
 VAFA_API int vafa_check_active_have_keys(const int64_t *cu_q, const int64_t *cu_k, int64_t n1);

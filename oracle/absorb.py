@@ -42,26 +42,38 @@ def project_u(q_raw, W_Q, W_K, dtype=np.float32):
     return np.einsum("thd,khd->thk", qp, W_K)
 
 
+def _per_head(a, W):
+    """einsum('thf,fhd->thd', a, W) as one 2-D product per head."""
+    T, H, _ = a.shape
+    out = np.empty((T, H, W.shape[2]), dtype=np.result_type(a, W))
+    for h in range(H):
+        out[:, h, :] = a[:, h, :] @ W[:, h, :]
+    return out
+
+
 def forward(u, X, W_V, cu_q, cu_k, scale, dtype=np.float32, return_ax=False):
-    """Inner op: returns ``(O [T_q,H,D_H], lse [T_q,H])`` (and aX if asked)."""
+    """Inner op: returns ``(O [T_q,H,D_H], lse [T_q,H])`` (and aX if asked).
+
+    Per segment the (token, head) rows are one ``[Lq*H, D_KV]`` matrix, so
+    scores and P.X are plain 2-D products against the segment's X rows.
+    """
     u = np.asarray(u, dtype=dtype)
     X = np.asarray(X, dtype=dtype)
     W_V = np.asarray(W_V, dtype=dtype)
     T_q, H, D_KV = u.shape
-    D_H = W_V.shape[2]
     ax = np.zeros((T_q, H, D_KV), dtype=dtype)
     lse = np.full((T_q, H), -np.inf, dtype=dtype)
     for q0, q1, k0, k1 in _segs(cu_q, cu_k):
         if q1 == q0 or k1 == k0:
             continue
-        s = np.einsum("thf,jf->thj", u[q0:q1], X[k0:k1]) * dtype(scale)
+        xs = X[k0:k1]
+        s = (u[q0:q1].reshape(-1, D_KV) @ xs.T) * dtype(scale)      # [Lq*H, Lk]
         m = s.max(axis=-1, keepdims=True)
         e = np.exp(s - m)
         l = e.sum(axis=-1, keepdims=True)
-        p = e / l
-        ax[q0:q1] = np.einsum("thj,jf->thf", p, X[k0:k1])
-        lse[q0:q1] = (m[..., 0] + np.log(l[..., 0])) * dtype(LOG2E)
-    O = np.einsum("thf,fhd->thd", ax, W_V).astype(dtype)
+        ax[q0:q1] = ((e / l) @ xs).reshape(q1 - q0, H, D_KV)
+        lse[q0:q1] = ((m[:, 0] + np.log(l[:, 0])) * dtype(LOG2E)).reshape(q1 - q0, H)
+    O = _per_head(ax, W_V).astype(dtype)
     if return_ax:
         return O, lse, ax
     return O, lse
@@ -73,27 +85,32 @@ def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
     X = np.asarray(X, dtype=dtype)
     W_V = np.asarray(W_V, dtype=dtype)
     dO = np.asarray(dO, dtype=dtype)
+    T_q, H, D_KV = u.shape
     sc = dtype(scale)
     du = np.zeros_like(u)
     dX = np.zeros_like(X)
-    dW_V = np.zeros_like(W_V)
-    dax_all = np.einsum("thd,fhd->thf", dO, W_V)
+    ax_all = np.zeros_like(u)
+    dax_all = np.empty_like(u)                                   # dO W_V^T per head
+    for h in range(H):
+        dax_all[:, h, :] = dO[:, h, :] @ W_V[:, h, :].T
     for q0, q1, k0, k1 in _segs(cu_q, cu_k):
         if q1 == q0 or k1 == k0:
             continue
         xs = X[k0:k1]
-        s = np.einsum("thf,jf->thj", u[q0:q1], xs) * sc
+        u2 = u[q0:q1].reshape(-1, D_KV)                          # [Lq*H, D_KV]
+        dax = dax_all[q0:q1].reshape(-1, D_KV)
+        s = (u2 @ xs.T) * sc
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
-        p /= p.sum(axis=-1, keepdims=True)                     # [Lq, H, Lk]
-        ax = np.einsum("thj,jf->thf", p, xs)
-        dax = dax_all[q0:q1]
-        dp = np.einsum("thf,jf->thj", dax, xs)
+        p /= p.sum(axis=-1, keepdims=True)                       # [Lq*H, Lk]
+        ax_all[q0:q1] = (p @ xs).reshape(q1 - q0, H, D_KV)
+        dp = dax @ xs.T
         ds = p * (dp - (p * dp).sum(axis=-1, keepdims=True))
-        du[q0:q1] = np.einsum("thj,jf->thf", ds, xs) * sc
-        dX[k0:k1] = (np.einsum("thj,thf->jf", ds, u[q0:q1]) * sc
-                     + np.einsum("thj,thf->jf", p, dax))
-        dW_V += np.einsum("thf,thd->fhd", ax, dO[q0:q1])
+        du[q0:q1] = ((ds @ xs) * sc).reshape(q1 - q0, H, D_KV)
+        dX[k0:k1] = (ds.T @ u2) * sc + p.T @ dax
+    dW_V = np.empty_like(W_V)
+    for h in range(H):
+        dW_V[:, h, :] = ax_all[:, h, :].T @ dO[:, h, :]
     return du, dX, dW_V
 
 

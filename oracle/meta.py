@@ -46,6 +46,21 @@ def validate_cu_seqlens(cu, T: int, name: str) -> None:
         raise ValueError(f"{name} must be non-decreasing (found negative segment length)")
 
 
+def validate_cu_seqlens_absorb(cu, T: int, name: str) -> None:
+    """ta/interface.py:92-106: the same checks as the varlen rule, with the
+    absorb operator's texts (1-D with len>=2, [0]==0, [-1]==T, non-decreasing)."""
+    c = np.asarray(cu)
+    if c.ndim != 1 or c.size < 2:
+        raise ValueError(f"{name}: must be 1-D with len>=2, got {tuple(c.shape)}")
+    c = c.astype(np.int64)
+    if c[0] != 0:
+        raise ValueError(f"{name}[0] must be 0")
+    if c[-1] != T:
+        raise ValueError(f"{name}[-1] must equal total tokens {T}, got {int(c[-1])}")
+    if (np.diff(c) < 0).any():
+        raise ValueError(f"{name} must be non-decreasing")
+
+
 def active_segments_have_keys(cu_q, cu_k) -> None:
     """ta/interface.py:109-116: q_len>0 requires k_len>0."""
     lq = np.diff(np.asarray(cu_q, dtype=np.int64))

@@ -155,6 +155,31 @@ def test_prepared_indices_fast_path(device):
     assert torch.equal(a, b)
 
 
+def test_prepared_indices_follow_the_call_cu_seqlens(device):
+    """Tables prepared for one batch, passed with validate=False alongside the
+    cu_seqlens of another batch whose segments have the same block counts but
+    other lengths (and larger totals), give that batch's result: the reference
+    kernels read the cu_seqlens of each call, so the plan must follow them."""
+    q_a, k_a = [7, 8, 6, 9], [200, 100, 150, 64]
+    q_b, k_b = [9, 16, 1, 12], [256, 128, 192, 64]   # same ceil(L/16), ceil(L/64)
+    ins = [t.to(device, torch.bfloat16) for t in make_inputs(q_b, k_b)]
+    cq_a, ck_a = cu_from_lens(q_a).to(device), cu_from_lens(k_a).to(device)
+    cq_b, ck_b = cu_from_lens(q_b).to(device), cu_from_lens(k_b).to(device)
+    qi, ki = prepare_target_attn_indices(cq_a, ck_a)
+    qi_b, ki_b = prepare_target_attn_indices(cq_b, ck_b)
+    assert torch.equal(qi, qi_b) and torch.equal(ki, ki_b)
+    fresh = packed_target_attn(*ins, cu_seqlens_q=cq_b, cu_seqlens_k=ck_b)
+    reused = packed_target_attn(*ins, cu_seqlens_q=cq_b, cu_seqlens_k=ck_b,
+                                q_chunk_indices=qi, k_chunk_indices=ki, validate=False)
+    assert torch.equal(fresh, reused)
+    # an in-place change of the prepared tensors is seen too
+    cq_a.copy_(cq_b)
+    ck_a.copy_(ck_b)
+    again = packed_target_attn(*ins, cu_seqlens_q=cq_a, cu_seqlens_k=ck_a,
+                               q_chunk_indices=qi, k_chunk_indices=ki, validate=False)
+    assert torch.equal(fresh, again)
+
+
 def test_prepared_indices_issue_no_device_sync(device):
     """The prepare_target_attn_indices + validate=False contract
     (ta/interface.py:125-138): the host cu_seqlens captured by the prepare
@@ -204,13 +229,22 @@ def test_absorb_deterministic(device):
 
 
 def test_absorb_validation_errors(device):
+    """The absorb operator's own texts (ta/interface.py:98-116), not the varlen ones."""
     ins = [t.to(device) for t in make_inputs([2, 3], [4, 5])]
-    with pytest.raises(ValueError, match="k_len > 0"):
-        packed_target_attn(*ins, cu_seqlens_q=torch.tensor([0, 2, 5], device=device),
-                           cu_seqlens_k=torch.tensor([0, 9, 9], device=device))
-    with pytest.raises(ValueError):
-        packed_target_attn(*ins, cu_seqlens_q=torch.tensor([0, 2, 6], device=device),
-                           cu_seqlens_k=torch.tensor([0, 4, 9], device=device))
+    t = lambda *x: torch.tensor(x, device=device)
+    cases = [
+        (t(0, 2, 5), t(0, 9, 9), "segments with q_len > 0 must have k_len > 0"),
+        (t(0, 2, 6), t(0, 4, 9), "cu_seqlens_q[-1] must equal total tokens 5, got 6"),
+        (t(1, 2, 5), t(0, 4, 9), "cu_seqlens_q[0] must be 0"),
+        (t(0, 4, 3, 5), t(0, 4, 4, 9), "cu_seqlens_q must be non-decreasing"),
+        (t(0, 2, 5), t(0, 6, 5, 9)[:3], "cu_seqlens_k[-1] must equal total tokens 9, got 5"),
+    ]
+    for cq, ck, text in cases:
+        with pytest.raises(ValueError) as e:
+            packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck)
+        assert str(e.value) == text, (str(e.value), text)
+    with pytest.raises(AssertionError, match="segment count mismatch q vs k"):
+        packed_target_attn(*ins, cu_seqlens_q=t(0, 2, 5), cu_seqlens_k=t(0, 9))
 
 
 def test_absorb_bf16_flag_3d_inputs_and_seqinfo(device):

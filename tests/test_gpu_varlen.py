@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import varlen as ov
-from parity import assert_close
+from parity import assert_close, check, report
 from varlenabsorbflashattn_amd import packed_varlen_attn, set_validate_cu_seqlens
 from varlenabsorbflashattn_amd.workloads import cu_from_lens
 
@@ -87,7 +87,9 @@ def test_varlen_config1_fp32(device):
 def test_varlen_input_scales(device, dist):
     """Stress distributions of fa-tools/benchmark_packed_varlen_flash_attn.py:226-233."""
     got, ref = run_case([100, 37], [300, 64], 4, 64, torch.bfloat16, device, dist_scale=dist)
-    assert_close("o", got[0], ref[0])
+    # scaled q/k make the softmax nearly one-hot, so O approaches single V rows
+    # (|v| up to ~5): errors are taken relative to max(1, rms(O))
+    assert_close("o", got[0], ref[0], rel=True)
 
 
 def test_single_key_returns_v(device):
@@ -293,14 +295,15 @@ def test_noncontiguous_inputs_match_contiguous(device):
 
 
 def _gpu_errors(out, ref):
-    """The parity.py metric evaluated on the GPU (for tensors too large to
-    move to the host): max of |out - ref| minus the rounding of ref to the
-    output dtype, and mean |out - ref|, both divided by max(1, rms(ref))."""
+    """The parity.py metrics evaluated on the GPU (for tensors too large to
+    move to the host): raw max and mean of |out - ref|, the largest rounding
+    of ref to the output dtype, and max(|out - ref| - that rounding)."""
     a, r = out.detach().float(), ref.detach().float()
     floor = (r.to(out.dtype).float() - r).abs()
-    s = max(1.0, r.pow(2).mean().sqrt().item())
     d = (a - r).abs()
-    return (d - floor).max().item() / s, d.mean().item() / s
+    return dict(max_abs=d.max().item(), mean_abs=d.mean().item(), floor=floor.max().item(),
+                excess=(d - floor).max().item(), rms=r.pow(2).mean().sqrt().item(),
+                ref_max=r.abs().max().item())
 
 
 def test_varlen_business_scale(device):
@@ -346,6 +349,6 @@ def test_varlen_business_scale(device):
         k0 += lk
     for name, a, r in (("o", o, o_r), ("dq", qd.grad, dq_r), ("dk", kd.grad, dk_r),
                        ("dv", vd.grad, dv_r)):
-        mx, mn = _gpu_errors(a, r)
-        print(f"  {name:8s} max_excess={mx:.3e} mean_abs={mn:.3e}")
-        assert mx <= 2e-2 and mn <= 2e-3, f"{name}: max {mx:.3e} mean {mn:.3e}"
+        e = _gpu_errors(a, r)
+        report(name, e, torch.bfloat16)
+        check(name, e, torch.bfloat16)

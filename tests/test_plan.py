@@ -74,19 +74,45 @@ def test_seqinfo_to_cu_errors_match(bad):
     assert str(e_ref.value).split()[0] == str(e_new.value).split()[0]
 
 
-@pytest.mark.parametrize("cu,T", [([0, 3, 5], 5), ([1, 3, 5], 5), ([0, 3, 4], 5),
-                                  ([0, 4, 3, 5], 5), ([0], 0)])
-def test_validate_cu_matches_oracle(cu, T):
-    ref_err = new_err = None
+# (cu, T, expected varlen text, expected absorb text); None = valid.  The texts
+# are the reference's: fa/interface.py:108-118 and ta/interface.py:98-106.
+VALIDATE_CASES = [
+    ([0, 3, 5], 5, None, None),
+    ([0, 3, 3, 5], 5, None, None),
+    ([1, 3, 5], 5, "cu_seqlens_q[0] must be 0, got 1", "cu_seqlens_q[0] must be 0"),
+    ([0, 3, 4], 5, "cu_seqlens_q[-1] must equal total tokens 5, got 4",
+     "cu_seqlens_q[-1] must equal total tokens 5, got 4"),
+    ([0, 4, 3, 5], 5, "cu_seqlens_q must be non-decreasing (found negative segment length)",
+     "cu_seqlens_q must be non-decreasing"),
+    ([0], 0, "cu_seqlens_q: must have at least 2 elements (n_seg+1 with n_seg>=1)",
+     "cu_seqlens_q: must be 1-D with len>=2, got (1,)"),
+    # the first failing rule wins: [0] before [-1] before monotonicity
+    ([2, 1, 9], 5, "cu_seqlens_q[0] must be 0, got 2", "cu_seqlens_q[0] must be 0"),
+    ([0, 7, 3], 5, "cu_seqlens_q[-1] must equal total tokens 5, got 3",
+     "cu_seqlens_q[-1] must equal total tokens 5, got 3"),
+]
+
+
+def _outcome(fn, cu, T):
     try:
-        meta.validate_cu_seqlens(np.array(cu), T, "cu_seqlens_q")
+        fn(np.array(cu), T, "cu_seqlens_q")
     except ValueError as e:
-        ref_err = str(e)
-    try:
-        _lib.validate_cu(np.array(cu), T, "cu_seqlens_q")
-    except ValueError as e:
-        new_err = str(e)
-    assert ref_err == new_err
+        return str(e)
+    return None
+
+
+@pytest.mark.parametrize("cu,T,fa_text,ta_text", VALIDATE_CASES)
+def test_validate_cu_varlen_texts(cu, T, fa_text, ta_text):
+    """Oracle and product both give the varlen operator's exact outcome."""
+    assert _outcome(meta.validate_cu_seqlens, cu, T) == fa_text
+    assert _outcome(_lib.validate_cu, cu, T) == fa_text
+
+
+@pytest.mark.parametrize("cu,T,fa_text,ta_text", VALIDATE_CASES)
+def test_validate_cu_absorb_texts(cu, T, fa_text, ta_text):
+    """Oracle and product both give the absorb operator's exact outcome."""
+    assert _outcome(meta.validate_cu_seqlens_absorb, cu, T) == ta_text
+    assert _outcome(_lib.validate_cu_absorb, cu, T) == ta_text
 
 
 def test_active_segments_have_keys():
@@ -298,3 +324,29 @@ def test_absorb_kv_resident_items_lead():
         assert cost == sorted(cost, reverse=True)
     # varlen plans have no such split
     assert int(_lib.plan_varlen(_cu([5, 7]), _cu([5, 7]), 2, 64).info.n_kv_res) == 0
+
+
+# ---- plans of the benchmark configurations ----------------------------------------
+
+def test_config_plans():
+    """The plans bench.py runs: C2 needs no key split (L <= 4096); every C3
+    (sequence, head) has 4-16 key chunks merged by one combine item, as the
+    config prescribes; C4 and C5 keep every sample's key range whole.  Each
+    plan also passes the coverage invariants above."""
+    from varlenabsorbflashattn_amd import workloads as W
+    c2 = W.config2(seed=0)
+    p2 = _lib.plan_varlen(_cu(c2.q_lens), _cu(c2.k_lens), c2.H, c2.D)
+    assert p2.info.n_comb == 0 and np.all(p2.section("fwd")[:, 4] == -1)
+    c3 = W.config3(seed=0)
+    p3 = _lib.plan_varlen(_cu(c3.q_lens), _cu(c3.k_lens), c3.H, c3.D)
+    fwd, comb = p3.section("fwd"), p3.section("comb")
+    assert len(comb) == len(c3.q_lens)          # one query tile per sequence (Lq <= 16)
+    assert np.all(fwd[:, 4] >= 0)
+    assert 4 <= fwd[:, 7].min() and fwd[:, 7].max() <= 16
+    lk = np.asarray(c3.k_lens)
+    want = np.clip(-(-lk // 2048), 4, 16)
+    assert np.array_equal(comb[np.argsort(comb[:, 4]), 3], want)
+    check_varlen_plan(c3.q_lens[:40], c3.k_lens[:40], H=c3.H, D=c3.D)
+    for cfg in (W.config4(seed=0), W.config5(seed=0)):
+        p = _lib.plan_absorb(_cu(cfg.q_lens), _cu(cfg.k_lens), cfg.H, cfg.D_in, cfg.D_H)
+        assert p.info.n_comb == 0 and p.info.max_split == 1, cfg.name

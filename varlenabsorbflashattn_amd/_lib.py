@@ -52,6 +52,7 @@ _SIGS = {
     "vafa_last_error": (C.c_char_p, []),
     "vafa_seqinfo_to_cu": (C.c_int, [_PI64, _I64, _PI32]),
     "vafa_validate_cu": (C.c_int, [_PI64, _I64, _I64, C.c_char_p]),
+    "vafa_validate_cu_absorb": (C.c_int, [_PI64, _I64, _I64, C.c_char_p]),
     "vafa_check_active_have_keys": (C.c_int, [_PI64, _PI64, _I64]),
     "vafa_chunk_indices": (C.c_int, [_PI64, _I64, _I32, _PI32, _I64, _PI64]),
     "vafa_plan_varlen": (C.c_int, [_PI64, _PI64, _I64, _I64, _I64, _PI32, _I64, _PINFO]),
@@ -158,8 +159,15 @@ def seqinfo_to_cu(seqinfo: np.ndarray) -> np.ndarray:
 
 
 def validate_cu(cu: np.ndarray, T: int, name: str) -> None:
+    """The varlen operator's cu_seqlens checks and texts (fa/interface.py:96-118)."""
     c = np.ascontiguousarray(cu, dtype=np.int64)
     check(lib().vafa_validate_cu(_i64p(c), c.size, int(T), name.encode()))
+
+
+def validate_cu_absorb(cu: np.ndarray, T: int, name: str) -> None:
+    """The absorb operator's cu_seqlens checks and texts (ta/interface.py:92-106)."""
+    c = np.ascontiguousarray(cu, dtype=np.int64)
+    check(lib().vafa_validate_cu_absorb(_i64p(c), c.size, int(T), name.encode()))
 
 
 def check_active_have_keys(cu_q: np.ndarray, cu_k: np.ndarray) -> None:
@@ -236,18 +244,25 @@ _CACHE_MAX = 64
 
 
 def device_plan(kind: str, cu_q: np.ndarray, cu_k: np.ndarray, dims: tuple, device) -> DevicePlan:
+    """The cached device plan for these cu_seqlens, marked as in use on the
+    current stream: a plan evicted from the cache while a kernel on another
+    stream still reads it keeps its memory until that stream's work is done."""
+    import torch
     key = (kind, cu_q.tobytes(), cu_k.tobytes(), dims, str(device))
     with _lock:
-        hit = _CACHE.get(key)
-        if hit is not None:
+        dp = _CACHE.get(key)
+        if dp is not None:
             _CACHE.move_to_end(key)
-            return hit
-    host = plan_varlen(cu_q, cu_k, *dims) if kind == "varlen" else plan_absorb(cu_q, cu_k, *dims)
-    dp = DevicePlan(host, device)
-    with _lock:
-        _CACHE[key] = dp
-        while len(_CACHE) > _CACHE_MAX:
-            _CACHE.popitem(last=False)
+    if dp is None:
+        host = (plan_varlen(cu_q, cu_k, *dims) if kind == "varlen"
+                else plan_absorb(cu_q, cu_k, *dims))
+        dp = DevicePlan(host, device)
+        with _lock:
+            _CACHE[key] = dp
+            while len(_CACHE) > _CACHE_MAX:
+                _CACHE.popitem(last=False)
+    if dp.items.is_cuda:
+        dp.items.record_stream(torch.cuda.current_stream(dp.items.device))
     return dp
 
 

@@ -27,23 +27,45 @@ _BT_Q_FWD = 16
 _BT_K_BWD = 64
 
 # prepare_target_attn_indices() remembers the host cu_seqlens behind the
-# tables it returns, so a later validate=False call needs no device->host copy.
-# Keyed by id() with a weak reference to the table (tensors compare by value).
+# tables it returns, so a later validate=False call on the SAME, unmodified
+# cu_seqlens tensors needs no device->host copy.  Keyed by id() of the query
+# table with a weak reference to it; the cu_seqlens tensors are held by weak
+# reference together with their version counters and data pointers, so any
+# other pair of tensors (or an in-place change of these) takes the copy again.
 _HOST_CU: dict = {}
 
 
-def _remember_host_cu(table: torch.Tensor, cu_q_h: np.ndarray, cu_k_h: np.ndarray) -> None:
+def _cu_stamp(t):
+    if not isinstance(t, torch.Tensor):
+        return None
+    return (weakref.ref(t), t._version, t.data_ptr())
+
+
+def _stamp_matches(stamp, t) -> bool:
+    if stamp is None or not isinstance(t, torch.Tensor):
+        return False
+    ref, version, data_ptr = stamp
+    return ref() is t and t._version == version and t.data_ptr() == data_ptr
+
+
+def _remember_host_cu(table: torch.Tensor, cu_q, cu_k, cu_q_h: np.ndarray,
+                      cu_k_h: np.ndarray) -> None:
     key = id(table)
-    _HOST_CU[key] = (weakref.ref(table, lambda _r, k=key: _HOST_CU.pop(k, None)), cu_q_h, cu_k_h)
+    _HOST_CU[key] = (weakref.ref(table, lambda _r, k=key: _HOST_CU.pop(k, None)),
+                     _cu_stamp(cu_q), _cu_stamp(cu_k), cu_q_h, cu_k_h)
 
 
-def _recall_host_cu(table: Optional[torch.Tensor]):
+def _recall_host_cu(table: Optional[torch.Tensor], cu_q, cu_k):
+    """Host copies taken when ``table`` was prepared, if ``cu_q`` / ``cu_k`` are
+    the very tensors it was prepared from, unmodified since; else None."""
     if table is None:
         return None
     hit = _HOST_CU.get(id(table))
     if hit is None or hit[0]() is not table:
         return None
-    return hit[1], hit[2]
+    if not (_stamp_matches(hit[1], cu_q) and _stamp_matches(hit[2], cu_k)):
+        return None
+    return hit[3], hit[4]
 
 
 def _select_fwd_mode() -> str:
@@ -74,7 +96,7 @@ def _validate_cu_seqlens(cu_host: np.ndarray, shape, T: int, name: str) -> None:
     """ta/interface.py:92-106."""
     if len(shape) != 1 or cu_host.size < 2:
         raise ValueError(f"{name}: must be 1-D with len>=2, got {tuple(shape)}")
-    _lib.validate_cu(cu_host, T, name)
+    _lib.validate_cu_absorb(cu_host, T, name)
 
 
 def _next_power_of_2(x: int) -> int:
@@ -87,13 +109,17 @@ def prepare_target_attn_indices(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.
     """Chunk tables ``(q_idx [NT_q,2], k_idx [NT_k,2])`` (ta/interface.py:125-138).
 
     Same content as the reference (BT_Q=16, BT_K=64 rows ``(seg, block)``).
-    Passing them back with ``validate=False`` skips every host round trip:
-    the host cu_seqlens captured here are reused to look up the cached plan.
+    Passing them back with ``validate=False`` together with the same
+    cu_seqlens tensors skips every host round trip: the host cu_seqlens
+    captured here are reused to look up the cached plan.  With other (or
+    modified) cu_seqlens tensors the call copies them to the host again, so
+    the plan always follows the cu_seqlens of the call, as the reference's
+    kernels do (they read cu_seqlens on every call).
     """
     cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
     q_idx = torch.from_numpy(_lib.chunk_indices(cu_q_h, _BT_Q_FWD)).to(cu_seqlens_q.device)
     k_idx = torch.from_numpy(_lib.chunk_indices(cu_k_h, _BT_K_BWD)).to(cu_seqlens_k.device)
-    _remember_host_cu(q_idx, cu_q_h, cu_k_h)
+    _remember_host_cu(q_idx, cu_seqlens_q, cu_seqlens_k, cu_q_h, cu_k_h)
     return q_idx, k_idx
 
 
@@ -119,12 +145,12 @@ class _TargetAttnFunction(torch.autograd.Function):
         assert H == H_wv, f"H mismatch: u={H}, W_V={H_wv}"
         assert u.dtype == X.dtype == W_V.dtype, \
             f"u/X/W_V must share dtype, got {u.dtype}/{X.dtype}/{W_V.dtype}"
-        assert u.is_cuda and X.is_cuda and W_V.is_cuda, "all inputs must be GPU tensors"
+        assert u.is_cuda and X.is_cuda and W_V.is_cuda, "all inputs must be CUDA"
         assert u.device == X.device == W_V.device, "u/X/W_V must be on same device"
         assert D_H in (16, 32, 64, 128, 256), f"D_H {D_H} not supported"
         dcode = _lib.dtype_code(u.dtype)
 
-        known = _recall_host_cu(q_chunk_indices)
+        known = _recall_host_cu(q_chunk_indices, cu_seqlens_q, cu_seqlens_k)
         if known is not None and not validate:
             cu_q_h, cu_k_h = known
         else:
@@ -138,7 +164,7 @@ class _TargetAttnFunction(torch.autograd.Function):
 
         u, X, W_V = (_aligned(t.contiguous()) for t in (u, X, W_V))
         B_DKV = _next_power_of_2(D_KV)
-        assert B_DKV <= 512, f"D_KV={D_KV} pads to {B_DKV}, which is too large"
+        assert B_DKV <= 512, f"D_KV={D_KV} pads to {B_DKV}, which is too large for v1 tiles"
 
         plan = _lib.device_plan("absorb", cu_q_h, cu_k_h, (H, D_KV, D_H), u.device)
         if plan.info.T_q > T_q or plan.info.T_k > T_k:

@@ -196,6 +196,20 @@ int vafa_validate_cu(const int64_t *cu, int64_t n1, int64_t T, const char *name)
   return VAFA_OK;
 }
 
+int vafa_validate_cu_absorb(const int64_t *cu, int64_t n1, int64_t T, const char *name) {
+  // same checks and order as vafa_validate_cu, with the absorb operator's texts
+  if (n1 < 2)
+    return fail(VAFA_ERR_VALUE, "%s: must be 1-D with len>=2, got (%lld,)", name,
+                (long long)(n1 < 0 ? 0 : n1));
+  if (cu[0] != 0) return fail(VAFA_ERR_VALUE, "%s[0] must be 0", name);
+  if (cu[n1 - 1] != T)
+    return fail(VAFA_ERR_VALUE, "%s[-1] must equal total tokens %lld, got %lld", name,
+                (long long)T, (long long)cu[n1 - 1]);
+  for (int64_t i = 0; i + 1 < n1; ++i)
+    if (cu[i + 1] < cu[i]) return fail(VAFA_ERR_VALUE, "%s must be non-decreasing", name);
+  return VAFA_OK;
+}
+
 int vafa_check_active_have_keys(const int64_t *cu_q, const int64_t *cu_k, int64_t n1) {
   for (int64_t i = 0; i + 1 < n1; ++i)
     if (cu_q[i + 1] - cu_q[i] > 0 && cu_k[i + 1] - cu_k[i] <= 0)

@@ -147,6 +147,23 @@ VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const 
                     int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
                     void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  vafa_varlen_fwd with its workspace replaced by a static
+ * device array of VAFA_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends: same arguments otherwise, same kernels, same results.  The caller
+ * still passes inputs, outputs and the device plan.  Plans whose split
+ * partials need more scratch than that return VAFA_ERR_WORKSPACE (use
+ * vafa_varlen_fwd with a workspace).  Calls no hipMalloc/hipFree; the stream
+ * must belong to the current device.  Every call on a GPU shares that GPU's
+ * array, so calls that overlap on one GPU (other streams, other threads)
+ * race: serialize them. */
+#define VAFA_NOALLOC_SCRATCH_BYTES (64ll << 20)
+VAFA_API int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o,
+                                     float *lse, const int32_t *plan_dev,
+                                     const vafa_plan_info *info, int64_t D, int32_t dtype,
+                                     float scale, void *stream);
+
 /* One stage of vafa_varlen_bwd, for callers that schedule the backward
  * themselves (e.g. dQ and dK/dV on two streams) and for per-kernel timing:
  *   VAFA_BWD_DELTA (0): delta = rowsum(O * dO) into the workspace;

@@ -26,6 +26,9 @@ VAFA_ERR_WORKSPACE = -4
 VAFA_ERR_CAPACITY = -5
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+# bytes of the static per-GPU scratch of vafa_varlen_fwd_noalloc
+# (VAFA_NOALLOC_SCRATCH_BYTES in include/vafa.h)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 PLAN_MAGIC = 0x56414641
 ITEM_INTS = 8
 
@@ -63,6 +66,8 @@ _SIGS = {
     "vafa_absorb_bwd_workspace": (C.c_int64, [_PINFO, _I64, _I64]),
     "vafa_varlen_fwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _PINFO, _I64, _I32, C.c_float,
                                   _P, _I64, _P]),
+    "vafa_varlen_fwd_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _P, _PINFO, _I64, _I32, C.c_float,
+                                          _P]),
     "vafa_varlen_bwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _PINFO, _I64, _I32,
                                   C.c_float, _P, _I64, _P]),
     "vafa_varlen_bwd_stage": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _PINFO, _I64,

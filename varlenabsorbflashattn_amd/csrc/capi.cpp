@@ -3,11 +3,20 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/vafa.h"
 #include "common.h"
 #include "kernels.h"
+
+// Device memory for the split-K partial rows of vafa_varlen_fwd_noalloc, for
+// callers that cannot allocate.  Each GPU holds its own copy of the array (a
+// code-object global) until the process ends.  Host code never passes
+// `scratch` itself to a kernel -- in host code the name is a stand-in, not a
+// device address: the device address is looked up once per device with
+// hipGetSymbolAddress (scratch_ptr below) and that pointer is used instead.
+static __device__ __align__(256) unsigned char scratch[VAFA_NOALLOC_SCRATCH_BYTES];
 
 namespace vafa {
 int fail(int code, const char *fmt, ...);
@@ -215,6 +224,35 @@ template <typename T> struct VBwdStage {
 template <typename T> struct AFwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_fwd_all<T>(a, s); } };
 template <typename T> struct ABwd { static void run(const AbsorbArgs &a, hipStream_t s) { absorb_bwd_all<T>(a, s); } };
 
+// ---- scratch of vafa_varlen_fwd_noalloc (the array is at file scope above) --
+constexpr int64_t kScratchBytes = VAFA_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+void *g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this GPU's scratch: looked up on the first call made
+// while that device is current, then reused.
+int scratch_ptr(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(VAFA_ERR_RUNTIME, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(VAFA_ERR_RUNTIME, "device ordinal %d beyond the %d the library tracks", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(VAFA_ERR_RUNTIME, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return VAFA_OK;
+}
+
 }  // namespace
 }  // namespace vafa
 
@@ -255,6 +293,26 @@ int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float 
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   if (int rc = by_dtype<VFwd>(dtype, a, (hipStream_t)stream)) return rc;
   return check_launch("vafa_varlen_fwd");
+}
+
+int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o, float *lse,
+                            const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                            int32_t dtype, float scale, void *stream) {
+  if (int rc = check_info(info, 1)) return rc;
+  if (!supported_d(D))
+    return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
+  const int64_t need = carve_varlen(nullptr, info, D, false).bytes;
+  if (need > kScratchBytes)
+    return fail(VAFA_ERR_WORKSPACE,
+                "vafa_varlen_fwd_noalloc: this plan's split partials need %lld bytes, the "
+                "static scratch holds %lld; call vafa_varlen_fwd with a workspace instead",
+                (long long)need, (long long)kScratchBytes);
+  void *ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_ptr(&ws)) return rc;
+  }
+  return vafa_varlen_fwd(q, k, v, o, lse, plan_dev, info, D, dtype, scale, ws,
+                         need > 0 ? kScratchBytes : 0, stream);
 }
 
 static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const void *v,

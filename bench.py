@@ -3,12 +3,16 @@
 Headline (``value``): packed varlen FlashAttention forward+backward TFLOP/s on
 configs[1] (H=16, D=128, bf16, 64 sequences with log-uniform lengths in
 [1, 4096], q = k lengths), FLOPs = 4 H D sum(L^2) forward + 10 H D sum(L^2)
-backward.  The same JSON line carries the secondary configurations (split-K
-forward, absorb forward GB/s), the roofline of the dominant kernel measured
-with HIP events on the launch stream, and the CPU baseline (the numpy oracle
-on a bounded sample of the same workload, timed on the host cores).
+backward (fa-tools/benchmark_packed_varlen_flash_attn.py:289-292).  The same
+JSON line carries the secondary configurations (split-K forward, absorb
+forward GB/s, fp32 and D=256 call shapes), the roofline of the dominant kernel
+measured with HIP events on the launch stream, and the CPU baseline (the numpy
+oracle on the host cores).  Every timed line reports mean, std, p50, p90, min
+and max over its timed iterations, each bracketed by HIP events (the
+reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c5,d256,copy,replay}
 """
 from __future__ import annotations
 
@@ -16,6 +20,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -24,78 +29,49 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_region(fn, iters, stream=None):
-    """Average ms of fn() over iters, with HIP events recorded on the launch stream."""
+def stats(ms):
+    """mean / std (population) / p50 / p90 / min / max of a list of ms."""
+    xs = sorted(ms)
+
+    def pct(q):
+        pos = (len(xs) - 1) * q
+        lo, hi = math.floor(pos), math.ceil(pos)
+        return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+    mean = sum(xs) / len(xs)
+    return {"mean": mean, "std": statistics.pstdev(xs) if len(xs) > 1 else 0.0,
+            "p50": pct(0.5), "p90": pct(0.9), "min": xs[0], "max": xs[-1], "n": len(xs)}
+
+
+def timed(fn, iters, warmup=1):
+    """Run fn() warmup times, then iters times with a HIP event pair around
+    each call, recorded on torch's current stream (the stream the C ABI
+    launches on).  Returns the stats of the per-call ms."""
     import torch
-    st = stream or torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(st)
-    for _ in range(iters):
-        fn()
-    e1.record(st)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / iters
-
-
-def bench_varlen_c2(steps, warmup):
-    import torch
-    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
-    case = W.config2(seed=0)
-    dev = torch.device("cuda:0")
-    q, k, v, do = W.varlen_tensors(case, dev, with_grad_out=True)
-    cu = W.cu_from_lens(case.q_lens, dev)
-    q.requires_grad_(True), k.requires_grad_(True), v.requires_grad_(True)
-
-    def step():
-        o = packed_varlen_attn(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu)
-        o.backward(do)
-        q.grad = k.grad = v.grad = None
-
-    def fwd():
-        with torch.no_grad():
-            packed_varlen_attn(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu)
-
     for _ in range(warmup):
-        step()
+        fn()
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
+    for a, b in evs:
+        a.record(st)
+        fn()
+        b.record(st)
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    fwd_ms = time_region(fwd, max(steps, 3))
-    # dominant kernel: dK/dV, timed with HIP events on the launch stream in the
-    # order of a training step (forward, delta, dQ, then dK/dV), so the figure
-    # matches what a kernel trace of the step reports
-    from varlenabsorbflashattn_amd.varlen import BackwardStages
-    stages = BackwardStages(q.detach(), k.detach(), v.detach(), do, cu, cu)
-    evs = []
-    for i in range(max(steps, 3) + 1):
-        fwd()
-        stages.run(0)
-        stages.run(1)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        stages.run(2)
-        e1.record()
-        if i > 0:  # the first round is a warmup
-            evs.append((e0, e1))
-    torch.cuda.synchronize()
-    dkv_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    del stages
-    flops = case.flops_fwd + case.flops_bwd
-    return case, ms, fwd_ms, flops, dkv_ms
+    return stats([a.elapsed_time(b) for a, b in evs])
 
 
-def bench_varlen_case(case, steps, warmup):
-    """fwd+bwd ms/step (wall clock around synchronized steps) and fwd ms (HIP events)."""
+# ---- varlen -------------------------------------------------------------------
+
+def _varlen_setup(case):
     import torch
     from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
     dev = torch.device("cuda:0")
@@ -112,6 +88,19 @@ def bench_varlen_case(case, steps, warmup):
         with torch.no_grad():
             packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
 
+    return (q, k, v, do, cq, ck), step, fwd
+
+
+def bench_varlen_c2(steps, warmup, case=None):
+    """C2 fwd+bwd: the contract's wall-clock ms/step over exactly `steps`
+    synchronized steps, plus per-step HIP-event stats, the forward alone, and
+    the dK/dV kernel (the roofline kernel) timed per launch in the order of a
+    training step (forward, delta, dQ, then dK/dV)."""
+    import torch
+    from varlenabsorbflashattn_amd import workloads as W
+    from varlenabsorbflashattn_amd.varlen import BackwardStages
+    case = case or W.config2(seed=0)
+    (q, k, v, do, cq, ck), step, fwd = _varlen_setup(case)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -120,16 +109,68 @@ def bench_varlen_case(case, steps, warmup):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    fwd_ms = time_region(fwd, steps)
-    del q, k, v, do
+    step_st = timed(step, steps, warmup=0)
+    fwd_st = timed(fwd, max(steps, 3))
+    stages = BackwardStages(q.detach(), k.detach(), v.detach(), do, cq, ck)
+    evs = []
+    for i in range(max(steps, 3) + 1):
+        fwd()
+        stages.run(0)
+        stages.run(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        stages.run(2)
+        e1.record()
+        if i > 0:  # the first round is a warmup
+            evs.append((e0, e1))
+    torch.cuda.synchronize()
+    dkv_st = stats([a.elapsed_time(b) for a, b in evs])
+    del stages, q, k, v, do
     torch.cuda.empty_cache()
-    return ms, fwd_ms
+    return case, ms, step_st, fwd_st, dkv_st
+
+
+def bench_varlen_case(case, steps, warmup):
+    """fwd+bwd per-step stats and forward stats (HIP events)."""
+    import torch
+    _, step, fwd = _varlen_setup(case)
+    step_st = timed(step, steps, warmup=warmup)
+    fwd_st = timed(fwd, steps)
+    torch.cuda.empty_cache()
+    return step_st, fwd_st
+
+
+def varlen_line(case, step_st, fwd_st):
+    tot = case.flops_fwd + case.flops_bwd
+    return {"sum_L_q": int(sum(case.q_lens)), "sum_L_k": int(sum(case.k_lens)),
+            "n_seq": len(case.q_lens), "H": case.H, "D": case.D,
+            "fwd_bwd_ms": step_st, "fwd_bwd_TFLOP/s": tot / (step_st["mean"] * 1e-3) / 1e12,
+            "fwd_ms": fwd_st, "fwd_TFLOP/s": case.flops_fwd / (fwd_st["mean"] * 1e-3) / 1e12,
+            "bwd_TFLOP/s": case.flops_bwd / ((step_st["mean"] - fwd_st["mean"]) * 1e-3) / 1e12}
+
+
+def bench_varlen_c3(iters):
+    import torch
+    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
+    case = W.config3(seed=0)
+    dev = torch.device("cuda:0")
+    q, k, v = W.varlen_tensors(case, dev)
+    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
+
+    def fwd():
+        with torch.no_grad():
+            packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+
+    st = timed(fwd, iters)
+    del q, k, v
+    torch.cuda.empty_cache()
+    return case, st
 
 
 def replay_records():
     """Production lengths sampled from the reference's fixtures
     (fa-fix/stage1_shapes.jsonl, ta-fix/real_shape_all.json) into tests/golden."""
-    g = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden")
+    g = os.path.join(ROOT, "tests", "golden")
     with open(os.path.join(g, "stage1_shapes_subset.jsonl")) as f:
         stage1 = [json.loads(line) for line in f if line.strip()]
     with open(os.path.join(g, "ta_real_shape_subset.json")) as f:
@@ -148,72 +189,57 @@ def bench_replay(steps, warmup):
     out = {"config": "replay", "stage1_H4_D64": [], "ta_real_dq968_dkv216": []}
     for r in stage1:
         case = W.VarlenCase(r["name"], r["q_lens"], r["k_lens"], 4, 64, torch.bfloat16)
-        ms, fwd_ms = bench_varlen_case(case, steps, warmup)
-        out["stage1_H4_D64"].append({
-            "name": r["name"], "segments": len(r["q_lens"]), "sum_lq": int(sum(r["q_lens"])),
-            "sum_lk": int(sum(r["k_lens"])), "fwd_ms": fwd_ms,
-            "fwd_TFLOP/s": case.flops_fwd / (fwd_ms * 1e-3) / 1e12, "fwd_bwd_ms": ms,
-            "fwd_bwd_TFLOP/s": (case.flops_fwd + case.flops_bwd) / (ms * 1e-3) / 1e12})
-        log(out["stage1_H4_D64"][-1])
+        step_st, fwd_st = bench_varlen_case(case, steps, warmup)
+        line = {"name": r["name"], **varlen_line(case, step_st, fwd_st)}
+        out["stage1_H4_D64"].append(line)
+        log({k: (v["mean"] if isinstance(v, dict) else v) for k, v in line.items()})
     for r in ta:
         case = W.AbsorbCase(r["tag"], r["q_lens"], r["k_lens"], 8, 32, int(r["d_kv"]),
                             torch.bfloat16)
-        a_ms = bench_absorb(case, max(steps, 3), d_q=int(r["d_q"]))
-        b_ms, bf_ms = bench_absorb_bwd(case, max(steps, 3), d_q=int(r["d_q"]))
-        gbs = case.bytes_fwd() / (a_ms * 1e-3) / 1e9
+        f_st = bench_absorb(case, max(steps, 3), d_q=int(r["d_q"]))
+        b_st, _ = bench_absorb_bwd(case, max(steps, 3), d_q=int(r["d_q"]))
+        gbs = case.bytes_fwd() / (f_st["mean"] * 1e-3) / 1e9
         out["ta_real_dq968_dkv216"].append({
             "name": r["tag"], "samples": len(r["q_lens"]), "sum_lq": int(sum(r["q_lens"])),
-            "sum_lk": int(sum(r["k_lens"])), "fwd_ms": a_ms, "fwd_GB/s": gbs,
-            "fwd_hbm_frac": gbs / HBM_PEAK_GBS, "fwd_bwd_ms": b_ms})
-        log(out["ta_real_dq968_dkv216"][-1])
+            "sum_lk": int(sum(r["k_lens"])), "fwd_ms": f_st, "fwd_GB/s": gbs,
+            "fwd_hbm_frac": gbs / HBM_PEAK_GBS, "fwd_bwd_ms": b_st})
+        log(out["ta_real_dq968_dkv216"][-1]["name"], f_st["mean"], b_st["mean"])
     return out
 
 
-def bench_varlen_c3(iters):
+# ---- absorb --------------------------------------------------------------------
+
+def _absorb_setup(case, d_q=None, dtype=None):
     import torch
-    from varlenabsorbflashattn_amd import packed_varlen_attn, workloads as W
-    case = W.config3(seed=0)
+    from varlenabsorbflashattn_amd import prepare_target_attn_indices
+    from varlenabsorbflashattn_amd import workloads as W
+    from varlenabsorbflashattn_amd.absorb import _project_u
     dev = torch.device("cuda:0")
-    q, k, v = W.varlen_tensors(case, dev)
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev, d_q=d_q, dtype=dtype)
     cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
-
-    def fwd():
-        with torch.no_grad():
-            packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
-
-    fwd()
-    ms = time_region(fwd, iters)
-    del q, k, v
-    torch.cuda.empty_cache()
-    return case, ms
+    with torch.no_grad():
+        u = _project_u(q_raw, W_Q, W_K).contiguous()
+    qi, ki = prepare_target_attn_indices(cq, ck)
+    return q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki
 
 
-def bench_absorb(case, iters, d_q=None, full=False):
+def bench_absorb(case, iters, d_q=None, full=False, dtype=None):
     """Inner absorb forward on precomputed u, through the reference's hot-path
     contract: prepare_target_attn_indices once, then validate=False calls
     (ta/interface.py:125-138) -- no host round trip inside the timed loop.
     With ``full``, also times the whole packed_target_attn forward (u
-    projection included) on the same inputs; returns (inner ms, full ms)."""
+    projection included) on the same inputs; returns (inner, full) stats."""
     import torch
-    from varlenabsorbflashattn_amd import (packed_target_attn, prepare_target_attn_indices,
-                                           target_attn_inner)
-    from varlenabsorbflashattn_amd import workloads as W
-    from varlenabsorbflashattn_amd.absorb import _project_u
-    dev = torch.device("cuda:0")
-    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev, d_q=d_q)
-    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
-    with torch.no_grad():
-        u = _project_u(q_raw, W_Q, W_K).contiguous()
+    from varlenabsorbflashattn_amd import packed_target_attn, target_attn_inner
+    q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case, d_q, dtype)
     scale = 1.0 / math.sqrt(case.D_H)
-    qi, ki = prepare_target_attn_indices(cq, ck)
 
     def fwd():
         with torch.no_grad():
             target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
 
-    fwd()
-    ms = time_region(fwd, iters)
-    full_ms = None
+    st = timed(fwd, iters)
+    full_st = None
     if full:
         def full_fwd():
             with torch.no_grad():
@@ -221,32 +247,24 @@ def bench_absorb(case, iters, d_q=None, full=False):
                                    q_chunk_indices=qi, k_chunk_indices=ki, scale=scale,
                                    validate=False)
 
-        full_fwd()
-        full_ms = time_region(full_fwd, iters)
+        full_st = timed(full_fwd, iters)
     del q_raw, X, u
     torch.cuda.empty_cache()
-    return (ms, full_ms) if full else ms
+    return (st, full_st) if full else st
 
 
-def bench_absorb_bwd(case, iters, d_q=None):
+def bench_absorb_bwd(case, iters, d_q=None, dtype=None):
     """Inner absorb forward + backward (grads of u, X, W_V) on precomputed u,
-    validate=False, with a fixed synthetic dO; returns (fwd+bwd ms, fwd ms)."""
+    validate=False, with a fixed synthetic dO; returns (fwd+bwd, fwd) stats."""
     import torch
-    from varlenabsorbflashattn_amd import prepare_target_attn_indices, target_attn_inner
-    from varlenabsorbflashattn_amd import workloads as W
-    from varlenabsorbflashattn_amd.absorb import _project_u
-    dev = torch.device("cuda:0")
-    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, dev, d_q=d_q)
-    cq, ck = W.cu_from_lens(case.q_lens, dev), W.cu_from_lens(case.k_lens, dev)
-    with torch.no_grad():
-        u = _project_u(q_raw, W_Q, W_K).contiguous()
+    from varlenabsorbflashattn_amd import target_attn_inner
+    q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case, d_q, dtype)
     u.requires_grad_(True)
     X.requires_grad_(True)
     W_V.requires_grad_(True)
     scale = 1.0 / math.sqrt(case.D_H)
-    qi, ki = prepare_target_attn_indices(cq, ck)
     g = torch.Generator().manual_seed(1)
-    dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(dev, torch.bfloat16)
+    dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(u.device, u.dtype)
 
     def step():
         o = target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
@@ -257,13 +275,24 @@ def bench_absorb_bwd(case, iters, d_q=None):
         with torch.no_grad():
             target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
 
-    step()
-    ms = time_region(step, iters)
-    f_ms = time_region(fwd, iters)
+    st = timed(step, iters)
+    f_st = timed(fwd, iters)
     del q_raw, X, u, dO
     torch.cuda.empty_cache()
-    return ms, f_ms
+    return st, f_st
 
+
+def absorb_line(case, st, full_st=None):
+    gbs = case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9
+    out = {"ms": st, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+           "TFLOP/s": case.flops_fwd / (st["mean"] * 1e-3) / 1e12,
+           "sum_lq": int(sum(case.q_lens)), "sum_lk": int(sum(case.k_lens))}
+    if full_st is not None:
+        out["packed_target_attn_ms"] = full_st
+    return out
+
+
+# ---- measurement support --------------------------------------------------------
 
 def roofline_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
@@ -276,64 +305,135 @@ def roofline_traffic():
         return None
 
 
-def cpu_baseline(budget_s=15.0):
-    """Oracle (numpy fp32) fwd+bwd on the shortest-first prefix of C2's segments
-    that fits the time budget; reported as TFLOP/s of that sample."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _blas_threads():
+    try:
+        import threadpoolctl
+        info = [i for i in threadpoolctl.threadpool_info() if i.get("user_api") == "blas"]
+        if info:
+            return int(info[0]["num_threads"])
+    except Exception:  # noqa: BLE001 - reporting only
+        pass
+    return None
+
+
+def _median_runs(fn, runs=3):
+    fn()  # warmup
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def cpu_baseline():
+    """The reference's CPU path restated (the numpy oracle, fp32) on the host
+    cores: 1 warmup + the median of 3 timed runs of each leg.
+      * varlen: forward + backward over all 64 segments of C2 (the workload
+        itself, fa/test_smoke.py:29-164), reported as TFLOP/s;
+      * absorb: the absorbed forward (ta/test_smoke.py:188-229) and the
+        explicit-K/V forward (ta/test_smoke.py:111-147) over the first 512 of
+        C4's 2048 samples, reported as GB/s of the same algorithmic bytes as
+        the GPU line (the reference's torch explicit/absorbed baselines,
+        ta/test_smoke.py:1353-1407)."""
     import numpy as np
+    import torch
+    from oracle import absorb as oa
     from oracle import varlen as ov
     from varlenabsorbflashattn_amd import workloads as W
     case = W.config2(seed=0)
-    rng = np.random.default_rng(0)
-    order = np.argsort(case.q_lens)
-    done_flops, t_used, n = 0.0, 0.0, 0
     H, D = case.H, case.D
-    for i in order:
-        L = int(case.q_lens[i])
-        q, k, v, do = (rng.standard_normal((L, H, D), dtype=np.float32) for _ in range(4))
-        cu = np.array([0, L])
-        t0 = time.perf_counter()
-        ov.forward(q, k, v, cu, cu, 1.0 / math.sqrt(D))
-        ov.backward(q, k, v, do, cu, cu, 1.0 / math.sqrt(D))
-        dt = time.perf_counter() - t0
-        t_used += dt
-        done_flops += 14.0 * H * D * L * L
-        n += 1
-        if t_used > budget_s:
-            break
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": done_flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"numpy fp32 oracle fwd+bwd on the {n} shortest of C2's 64 segments "
-                      f"(sum L^2 share {done_flops / (14.0 * H * D * float(np.dot(case.q_lens, case.q_lens))):.3f}), "
-                      f"{t_used:.1f} s"}
+    rng = np.random.default_rng(0)
+    T = sum(case.q_lens)
+    q, k, v, do = (rng.standard_normal((T, H, D), dtype=np.float32) for _ in range(4))
+    cu = np.zeros(len(case.q_lens) + 1, dtype=np.int64)
+    cu[1:] = np.cumsum(case.q_lens)
+    sc = 1.0 / math.sqrt(D)
 
+    def varlen_leg():
+        ov.forward(q, k, v, cu, cu, sc)
+        ov.backward(q, k, v, do, cu, cu, sc)
+
+    v_med, v_runs = _median_runs(varlen_leg)
+    flops = case.flops_fwd + case.flops_bwd
+
+    full4 = W.config4(seed=0)
+    sub = W.AbsorbCase("c4_first512", full4.q_lens[:512], full4.k_lens[:512], full4.H,
+                       full4.D_H, full4.D_in, torch.float32)
+    q_raw, X, W_Q, W_K, W_V = (t.numpy() for t in W.absorb_tensors(sub, "cpu"))
+    cq = np.concatenate([[0], np.cumsum(sub.q_lens)])
+    ck = np.concatenate([[0], np.cumsum(sub.k_lens)])
+    asc = 1.0 / math.sqrt(sub.D_H)
+    u = oa.project_u(q_raw, W_Q, W_K)
+    gpu_bytes = W.AbsorbCase("c4_first512_bf16", sub.q_lens, sub.k_lens, sub.H, sub.D_H,
+                             sub.D_in, torch.bfloat16).bytes_fwd()
+    a_med, a_runs = _median_runs(lambda: oa.forward(u, X, W_V, cq, ck, asc))
+    e_med, e_runs = _median_runs(
+        lambda: oa.explicit_forward(q_raw, X, W_Q, W_K, W_V, cq, ck, asc, np.float32))
+    return {"value": flops / v_med / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
+            "kind": "port",
+            "sample": f"numpy fp32 oracle forward+backward over all 64 C2 segments "
+                      f"(sum L^2 = {int(np.dot(case.q_lens, case.q_lens))}), median of "
+                      f"3 runs after 1 warmup: {v_med:.2f} s",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "runs_s": v_runs,
+            "absorb": {"sample": "first 512 of C4's 2048 samples, fp32 forward",
+                       "absorbed_fwd_s": a_med, "absorbed_fwd_GB/s": gpu_bytes / a_med / 1e9,
+                       "explicit_fwd_s": e_med, "explicit_fwd_GB/s": gpu_bytes / e_med / 1e9,
+                       "note": "GB/s uses the bf16 algorithmic bytes of the GPU line "
+                               "(the fp32 CPU run moves twice as many)",
+                       "runs_s": {"absorbed": a_runs, "explicit": e_runs}}}
+
+
+# ---- entry points ---------------------------------------------------------------
 
 def run_only(which, steps, warmup):
     """One configuration, for per-kernel profiling runs."""
+    import torch
     from varlenabsorbflashattn_amd import workloads as W
     if which == "copy":
         # calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE: a 1 GiB device copy
-        import torch
         x = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
         y = torch.empty_like(x)
-        ms = time_region(lambda: y.copy_(x), max(steps, 1))
-        return {"config": "copy_1GiB", "ms": ms, "GB/s": 2 * (1 << 30) / (ms * 1e-3) / 1e9}
-    if which == "c2":
-        case, ms, fwd_ms, flops, dkv_ms = bench_varlen_c2(steps, warmup)
-        return {"config": case.name, "ms_per_step": ms, "TFLOP/s": flops / (ms * 1e-3) / 1e12,
-                "fwd_ms": fwd_ms, "dkv_ms": dkv_ms}
+        st = timed(lambda: y.copy_(x), max(steps, 1))
+        return {"config": "copy_1GiB", "ms": st, "GB/s": 2 * (1 << 30) / (st["mean"] * 1e-3) / 1e9}
+    if which in ("c2", "c2_128k"):
+        case = W.config2(seed=0) if which == "c2" else W.config2_tokens(seed=0)
+        case, ms, step_st, fwd_st, dkv_st = bench_varlen_c2(steps, warmup, case)
+        return {"config": which, "ms_per_step": ms,
+                "TFLOP/s": (case.flops_fwd + case.flops_bwd) / (ms * 1e-3) / 1e12,
+                **varlen_line(case, step_st, fwd_st), "dkv_ms": dkv_st}
+    if which == "d256":
+        c = W.config2(seed=0)
+        case = W.VarlenCase("c2_lengths_H8_D256", c.q_lens, c.k_lens, 8, 256, torch.bfloat16)
+        step_st, fwd_st = bench_varlen_case(case, max(steps, 3), warmup)
+        return {"config": case.name, **varlen_line(case, step_st, fwd_st)}
     if which == "c3":
-        case, ms = bench_varlen_c3(max(steps, 1))
-        return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+        case, st = bench_varlen_c3(max(steps, 1))
+        return {"config": case.name, "ms": st,
+                "GB/s": case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9}
     if which == "replay":
         return bench_replay(max(steps, 1), warmup)
-    if which == "c4b":
+    if which in ("c4b", "c4_fp32"):
         case = W.config4(seed=0)
-        ms, f_ms = bench_absorb_bwd(case, max(steps, 1))
-        return {"config": case.name + "_fwd_bwd", "ms": ms, "fwd_ms": f_ms, "bwd_ms": ms - f_ms}
+        dt = torch.float32 if which == "c4_fp32" else None
+        st, f_st = bench_absorb_bwd(case, max(steps, 1), dtype=dt)
+        return {"config": case.name + ("_fp32" if dt else "") + "_fwd_bwd", "ms": st,
+                "fwd_ms": f_st, "bwd_ms": st["mean"] - f_st["mean"]}
     case = W.config4(seed=0) if which == "c4" else W.config5(seed=0)
-    ms = bench_absorb(case, max(steps, 1))
-    return {"config": case.name, "ms": ms, "GB/s": case.bytes_fwd() / (ms * 1e-3) / 1e9}
+    st = bench_absorb(case, max(steps, 1))
+    return {"config": case.name, **absorb_line(case, st)}
 
 
 def main():
@@ -345,7 +445,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4b", "c5", "copy", "replay"],
+    ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c5",
+                                       "d256", "copy", "replay"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -360,36 +461,53 @@ def main():
         print(json.dumps(run_only(args.only, args.steps, args.warmup)))
         return
 
-    case, ms, fwd_ms, flops, dkv_ms = bench_varlen_c2(args.steps, args.warmup)
-    tflops = flops / (ms * 1e-3) / 1e12
-    fwd_tflops = case.flops_fwd / (fwd_ms * 1e-3) / 1e12
+    case, ms, step_st, fwd_st, dkv_st = bench_varlen_c2(args.steps, args.warmup)
+    tflops = (case.flops_fwd + case.flops_bwd) / (ms * 1e-3) / 1e12
+    c2 = varlen_line(case, step_st, fwd_st)
     # dK/dV kernel: 4 GEMM passes (S recompute, dP, dV, dK) = 8 H D sum(L^2)
     dkv_flops = 2.0 * case.flops_fwd
-    dkv_tflops = dkv_flops / (dkv_ms * 1e-3) / 1e12
-    log(f"C2 fwd+bwd {ms:.3f} ms/step -> {tflops:.1f} TFLOP/s; fwd {fwd_ms:.3f} ms -> "
-        f"{fwd_tflops:.1f} TFLOP/s; dK/dV kernel {dkv_ms:.3f} ms -> {dkv_tflops:.1f} TFLOP/s")
+    dkv_tflops = dkv_flops / (dkv_st["mean"] * 1e-3) / 1e12
+    log(f"C2 fwd+bwd {ms:.3f} ms/step -> {tflops:.1f} TFLOP/s; fwd {fwd_st['mean']:.3f} ms -> "
+        f"{c2['fwd_TFLOP/s']:.1f} TFLOP/s; dK/dV kernel {dkv_st['mean']:.3f} ms -> "
+        f"{dkv_tflops:.1f} TFLOP/s")
     secondary = {}
     if not args.skip_secondary:
         from varlenabsorbflashattn_amd import workloads as W
-        c3, c3_ms = bench_varlen_c3(max(3, args.steps // 2))
+        n2 = max(3, args.steps // 2)
+        c3, c3_st = bench_varlen_c3(n2)
+        gbs = c3.bytes_fwd() / (c3_st["mean"] * 1e-3) / 1e9
         secondary["c3_varlen_splitk_fwd"] = {
-            "ms": c3_ms, "GB/s": c3.bytes_fwd() / (c3_ms * 1e-3) / 1e9,
-            "hbm_frac": c3.bytes_fwd() / (c3_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "TFLOP/s": c3.flops_fwd / (c3_ms * 1e-3) / 1e12}
-        log("C3", secondary["c3_varlen_splitk_fwd"])
+            "ms": c3_st, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "TFLOP/s": c3.flops_fwd / (c3_st["mean"] * 1e-3) / 1e12}
+        log("C3", c3_st["mean"], gbs)
         for cfg in (W.config4(seed=0), W.config5(seed=0)):
-            a_ms, full_ms = bench_absorb(cfg, max(3, args.steps // 2), full=True)
-            gbs = cfg.bytes_fwd() / (a_ms * 1e-3) / 1e9
-            secondary[cfg.name + "_fwd"] = {
-                "ms": a_ms, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-                "TFLOP/s": cfg.flops_fwd / (a_ms * 1e-3) / 1e12,
-                "packed_target_attn_ms": full_ms,
-                "sum_lq": int(sum(cfg.q_lens)), "sum_lk": int(sum(cfg.k_lens))}
-            log(cfg.name, secondary[cfg.name + "_fwd"])
+            st, full_st = bench_absorb(cfg, n2, full=True)
+            secondary[cfg.name + "_fwd"] = absorb_line(cfg, st, full_st)
+            log(cfg.name, st["mean"], secondary[cfg.name + "_fwd"]["GB/s"])
         c4 = W.config4(seed=0)
-        b_ms, bf_ms = bench_absorb_bwd(c4, max(3, args.steps // 2))
-        secondary[c4.name + "_fwd_bwd"] = {"ms": b_ms, "fwd_ms": bf_ms, "bwd_ms": b_ms - bf_ms}
-        log(c4.name + " fwd+bwd", secondary[c4.name + "_fwd_bwd"])
+        b_st, bf_st = bench_absorb_bwd(c4, n2)
+        secondary[c4.name + "_fwd_bwd"] = {"ms": b_st, "fwd_ms": bf_st,
+                                           "bwd_ms": b_st["mean"] - bf_st["mean"]}
+        log(c4.name + " fwd+bwd", b_st["mean"], bf_st["mean"])
+        # the reference's documented absorb call is fp32 (no bf16 flag)
+        b_st, bf_st = bench_absorb_bwd(c4, n2, dtype=torch.float32)
+        c4f = W.AbsorbCase(c4.name, c4.q_lens, c4.k_lens, c4.H, c4.D_H, c4.D_in, torch.float32)
+        secondary[c4.name + "_fp32_fwd_bwd"] = {
+            "ms": b_st, "fwd_ms": bf_st, "bwd_ms": b_st["mean"] - bf_st["mean"],
+            "fwd_GB/s": c4f.bytes_fwd() / (bf_st["mean"] * 1e-3) / 1e9}
+        log(c4.name + " fp32 fwd+bwd", b_st["mean"], bf_st["mean"])
+        # configs[1] text also says "about 128k total tokens": the same draw
+        # extended to 128 Ki tokens
+        c2k = W.config2_tokens(seed=0)
+        s_st, f_st = bench_varlen_case(c2k, n2, 3)
+        secondary["c2_varlen_fwd_bwd_128k_tokens"] = varlen_line(c2k, s_st, f_st)
+        log("C2 at 128k tokens", s_st["mean"], f_st["mean"])
+        # D=256 (fa/interface.py:167 accepts it) on C2's lengths at H=8
+        c256 = W.VarlenCase("c2_lengths_H8_D256", case.q_lens, case.k_lens, 8, 256,
+                            torch.bfloat16)
+        s_st, f_st = bench_varlen_case(c256, n2, 3)
+        secondary["varlen_d256_fwd_bwd"] = varlen_line(c256, s_st, f_st)
+        log("D=256", s_st["mean"], f_st["mean"])
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     out = {
         "metric": "varlen-FA fwd/bwd TFLOP/s + absorb-attn HBM GB/s, % of MI355X peak",
@@ -408,13 +526,14 @@ def main():
                                "log-uniform[1,4096], q=k lens, non-causal",
                    "seed": 0, "sum_L": int(sum(case.q_lens)),
                    "sum_L2": int(sum(x * x for x in case.q_lens))},
+        "step_ms": step_st,
         "roofline": {"bound": "mfma", "kernel": "varlen_dkv_kernel<bf16,128>",
                      "achieved": dkv_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": dkv_tflops / BF16_PEAK_TFLOPS, "traffic": roofline_traffic(),
                      "work_per_launch": "8*H*D*sum(L^2) = %.4g FLOP" % dkv_flops,
-                     "ms_per_launch": dkv_ms},
-        "forward_kernel": {"kernel": "varlen_fwd_kernel<bf16,128>", "ms": fwd_ms,
-                           "TFLOP/s": fwd_tflops, "frac": fwd_tflops / BF16_PEAK_TFLOPS},
+                     "ms_per_launch": dkv_st["mean"], "ms_stats": dkv_st,
+                     "timing": "HIP events on the launch stream around each dK/dV launch"},
+        "c2": c2,
         "secondary": secondary,
         "cpu_baseline": cpu,
     }

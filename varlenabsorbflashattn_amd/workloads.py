@@ -86,6 +86,17 @@ def config2(seed: int = 0, n_seq: int = 64) -> VarlenCase:
     return VarlenCase("c2_varlen_fwd_bwd", lens, lens, 16, 128, torch.bfloat16, seed)
 
 
+def config2_tokens(seed: int = 0, total: int = 128 * 1024) -> VarlenCase:
+    """configs[1] read by its token count ("about 128k total tokens"): the same
+    seeded log-uniform draw as config2 (whose 64 sequences are its prefix),
+    extended until the packed length reaches ``total`` tokens."""
+    rng = np.random.default_rng(seed)
+    lens = _log_uniform_int(rng, 1, 4096, 4096)
+    n = int(np.searchsorted(np.cumsum(lens), total)) + 1
+    lens = lens[:n].tolist()
+    return VarlenCase("c2_varlen_fwd_bwd_128k_tokens", lens, lens, 16, 128, torch.bfloat16, seed)
+
+
 def config3(seed: int = 0, n_seq: int = 256) -> VarlenCase:
     """Split-K forward: Lq ~ U{1..16}, Lk log-uniform in [1024, 32768], H=32, D=128."""
     rng = np.random.default_rng(seed)

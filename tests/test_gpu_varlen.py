@@ -203,7 +203,7 @@ def test_multi_seed(device, seed):
         assert_close(n, a, r)
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_backward_stages_match_fused(device, D):
     """vafa_varlen_bwd_stage (delta, dQ, dK/dV launched separately) reproduces
     vafa_varlen_bwd, whose dQ kernel forms delta itself, bit for bit."""

@@ -96,12 +96,14 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
                         a.comb_rows, st);
 }
 
-// Backward stages.  Matrix-core kernels for D in {32, 64, 128}; D=16 and
-// D=256 (whose dK/dV accumulators exceed the register file) take the
+// Backward stages.  Matrix-core kernels for D in {32, 64, 128, 256}; D=16
+// (below the 32-wide output tiles of the 32x32x16 products) and fp32 take the
 // wave-per-row kernels.
+inline bool mfma_bwd_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
 template <typename T>
 void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
-  const bool mfma = sizeof(T) == 2 && (a.D == 32 || a.D == 64 || a.D == 128);
+  const bool mfma = sizeof(T) == 2 && mfma_bwd_d(a.D);
   if (stage == VAFA_BWD_DELTA) {
     launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
   } else if (stage == VAFA_BWD_DQ) {
@@ -110,6 +112,7 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
         if (a.D == 32) launch_mfma_varlen_dq<T, 32>(a, st);
         if (a.D == 64) launch_mfma_varlen_dq<T, 64>(a, st);
         if (a.D == 128) launch_mfma_varlen_dq<T, 128>(a, st);
+        if (a.D == 256) launch_mfma_varlen_dq<T, 256>(a, st);
       }
     }
     if (!mfma) launch_simt_varlen_dq<T>(a, st);
@@ -120,6 +123,7 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
         if (a.D == 32) launch_mfma_varlen_dkv<T, 32>(a, st);
         if (a.D == 64) launch_mfma_varlen_dkv<T, 64>(a, st);
         if (a.D == 128) launch_mfma_varlen_dkv<T, 128>(a, st);
+        if (a.D == 256) launch_mfma_varlen_dkv<T, 256>(a, st);
       }
     }
     if (!mfma) launch_simt_varlen_dkv<T>(a, st);
@@ -130,7 +134,7 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
 // same bits as the delta stage) and leaves it for dK/dV.
 template <typename T>
 void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
-  const bool mfma = sizeof(T) == 2 && (a.D == 32 || a.D == 64 || a.D == 128);
+  const bool mfma = sizeof(T) == 2 && mfma_bwd_d(a.D);
   VarlenArgs f = a;
   f.fuse_delta = mfma;
   if (!mfma) varlen_bwd_stage<T>(VAFA_BWD_DELTA, f, st);

@@ -58,7 +58,7 @@ __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H,
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
@@ -181,7 +181,11 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
     }
     pb[0] = pack8<T>(s, 0);
     sb[0] = pack8<T>(dp, 0);
-    constexpr int kRowsPer = 8 / (2 * ND);  // second-half rows per first-half product
+    // the 8 second-half rows are spread over the first 2*ND products: kRowsPer
+    // rows at every kEvery-th product (one row every second product at D=256)
+    constexpr int kSteps = 2 * ND < 8 ? 2 * ND : 8;
+    constexpr int kRowsPer = 8 / kSteps;
+    constexpr int kEvery = 2 * ND / kSteps;
     auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
     auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
     float Ln[kRowsPer], Dn[kRowsPer];
@@ -197,25 +201,26 @@ __global__ __launch_bounds__(256, 2) void varlen_dkv_kernel(
       else
         adv[dt] = M::mma(a, pb[mm], adv[dt]);
       if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
-      if (i < 2 * ND) {
+      if (i < 2 * ND && i % kEvery == 0) {
+        const int g = i / kEvery;
         float Lc[kRowsPer], Dc[kRowsPer];
 #pragma unroll
         for (int rr = 0; rr < kRowsPer; ++rr) {
           Lc[rr] = Ln[rr], Dc[rr] = Dn[rr];
-          if (i + 1 < 2 * ND) {
-            const int rn = 8 + (i + 1) * kRowsPer + rr;
+          if (g + 1 < kSteps) {
+            const int rn = 8 + (g + 1) * kRowsPer + rr;
             Ln[rr] = lse_at(rn);
             Dn[rr] = del_at(rn);
           }
         }
 #pragma unroll
         for (int rr = 0; rr < kRowsPer; ++rr) {
-          const int r = 8 + i * kRowsPer + rr;
+          const int r = 8 + g * kRowsPer + rr;
           const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lc[rr]));
           s[r] = p;
           dp[r] = p * (dp[r] - Dc[rr]);
         }
-        if (i == 2 * ND - 1) {
+        if (g == kSteps - 1) {
           pb[1] = pack8<T>(s, 8);
           sb[1] = pack8<T>(dp, 8);
         }
@@ -507,6 +512,8 @@ VAFA_INST(bf16, 128)
 VAFA_INST(f16, 32)
 VAFA_INST(f16, 64)
 VAFA_INST(f16, 128)
+VAFA_INST(bf16, 256)
+VAFA_INST(f16, 256)
 #undef VAFA_INST
 
 }  // namespace vafa

@@ -43,8 +43,6 @@ def errors(out: torch.Tensor, ref: np.ndarray) -> dict:
 
 
 def _scale(e: dict, dtype, rel: bool) -> float:
-    if dtype == torch.float32 and not rel:
-        return 1.0
     return max(1.0, e["rms"]) if (rel or e["ref_max"] > ABS_LIMIT) else 1.0
 
 

@@ -99,19 +99,22 @@ def test_c3_subset_split_forward(device):
     assert_close("o", o, o_r)
 
 
-def _absorb_inputs(case, device):
-    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, device)
+def _absorb_inputs(case, device, dtype=None):
+    q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, device, dtype=dtype)
     with torch.no_grad():
         u = _project_u(q_raw, W_Q, W_K).contiguous()
     del q_raw
     return u, X, W_V
 
 
-def test_c4_full_fwd_bwd(device):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_c4_full_fwd_bwd(device, dtype):
+    """bf16 (the benchmark) and fp32, the reference's documented call (no bf16
+    flag: fp32 inputs, IEEE fp32 products)."""
     case = W.config4(seed=0)
-    print(f"[C4 full] samples={len(case.q_lens)} T_q={sum(case.q_lens)} "
+    print(f"[C4 full {dtype}] samples={len(case.q_lens)} T_q={sum(case.q_lens)} "
           f"T_k={sum(case.k_lens)}", flush=True)
-    u, X, W_V = _absorb_inputs(case, device)
+    u, X, W_V = _absorb_inputs(case, device, dtype)
     cq, ck = W.cu_from_lens(case.q_lens, device), W.cu_from_lens(case.k_lens, device)
     qi, ki = prepare_target_attn_indices(cq, ck)
     g = torch.Generator(device=device).manual_seed(11)
@@ -123,8 +126,10 @@ def test_c4_full_fwd_bwd(device):
     torch.cuda.synchronize()
     hu, hX, hW, hdO = (_host(t) for t in (u, X, W_V, dO))
     cq_h, ck_h = _cu_np(case.q_lens), _cu_np(case.k_lens)
-    O_r, _ = oa.forward(hu, hX, hW, cq_h, ck_h, scale, np.float32)
-    du_r, dX_r, dW_r = oa.backward(hu, hX, hW, hdO, cq_h, ck_h, scale, np.float32)
+    # float64 for the fp32 path (its own fp32 rounding is what is measured)
+    odt = np.float64 if dtype == torch.float32 else np.float32
+    O_r, _ = oa.forward(hu, hX, hW, cq_h, ck_h, scale, odt)
+    du_r, dX_r, dW_r = oa.backward(hu, hX, hW, hdO, cq_h, ck_h, scale, odt)
     for n, a, r in (("O", O, O_r), ("du", ud.grad, du_r), ("dX", Xd.grad, dX_r),
                     ("dW_V", Wd.grad, dW_r)):
         assert_close(n, a, r)

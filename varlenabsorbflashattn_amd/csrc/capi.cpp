@@ -160,7 +160,11 @@ AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t D
   if (!bwd) {
     w.part_o = c.take<float>(info->n_part_rows * H * DH * 4);
     w.part_lse = c.take<float>(info->n_part_rows * H * 4);
-    w.wvt = c.take<char>(mfma_absorb_wvt_elems((int)H, (int)F, (int)DH) * 2);
+    // W_V re-laid out for the projection: 16-bit (mfma_absorb_wvt_elems x 2
+    // bytes) or fp32 (f32_absorb_wvt_elems x 4 bytes); sized for either
+    const int64_t wvt16 = mfma_absorb_wvt_elems((int)H, (int)F, (int)DH) * 2;
+    const int64_t wvt32 = f32_absorb_wvt_elems((int)H, (int)F, (int)DH) * 4;
+    w.wvt = c.take<char>(wvt16 > wvt32 ? wvt16 : wvt32);
   } else {
     w.delta = c.take<float>(Tq * H * 4);
     w.dax = c.take<float>(Tq * H * F * 4);
@@ -182,7 +186,10 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
       launch_simt_absorb_fwd<T>(a, st);
     }
   } else {
-    launch_simt_absorb_fwd<T>(a, st);
+    if (f32_absorb_supported(a.H, a.F, a.DH))
+      launch_f32_absorb_fwd(a, st);
+    else
+      launch_simt_absorb_fwd<T>(a, st);
   }
   launch_lse_combine<T>(a.part_o, a.part_lse, a.O, a.lse, a.comb_items, a.n_comb, a.H, a.DH,
                         a.comb_rows, st);
@@ -204,6 +211,8 @@ void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
       launch_mfma_absorb_du<T>(a, st);
       launch_mfma_absorb_dx<T>(a, st);
     }
+  } else if (sizeof(T) == 4 && f32_absorb_supported(a.H, a.F, a.DH)) {
+    launch_f32_absorb_du_dx(a, st);
   } else {
     launch_simt_absorb_du<T>(a, st);
     launch_simt_absorb_dx<T>(a, st);

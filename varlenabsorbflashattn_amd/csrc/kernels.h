@@ -96,4 +96,11 @@ template <typename T> void launch_mfma_absorb_du(const AbsorbArgs &, hipStream_t
 template <typename T> bool launch_mfma_absorb_dax(const AbsorbArgs &, hipStream_t);
 template <typename T> void launch_mfma_absorb_dx(const AbsorbArgs &, hipStream_t);
 
+// absorb_f32.hip: fp32 absorb on fp32 matrix cores (v_mfma_f32_16x16x4_f32)
+bool f32_absorb_supported(int H, int F, int DH);
+int64_t f32_absorb_wvt_elems(int H, int F, int DH);
+void launch_f32_absorb_fwd(const AbsorbArgs &, hipStream_t);
+// du / aX (query side) and dX (key side); dAX and delta must be in the workspace
+void launch_f32_absorb_du_dx(const AbsorbArgs &, hipStream_t);
+
 }  // namespace vafa

@@ -12,7 +12,7 @@ and max over its timed iterations, each bracketed by HIP events (the
 reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c5,d256,copy,replay}
+       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c5,d256,fused,copy,replay}
 """
 from __future__ import annotations
 
@@ -147,6 +147,21 @@ def varlen_line(case, step_st, fwd_st):
             "fwd_bwd_ms": step_st, "fwd_bwd_TFLOP/s": tot / (step_st["mean"] * 1e-3) / 1e12,
             "fwd_ms": fwd_st, "fwd_TFLOP/s": case.flops_fwd / (fwd_st["mean"] * 1e-3) / 1e12,
             "bwd_TFLOP/s": case.flops_bwd / ((step_st["mean"] - fwd_st["mean"]) * 1e-3) / 1e12}
+
+
+def fused_case():
+    """64 segments of 16 queries against 8192 keys each, H=4, D=64: the
+    backward runs the fused key-major dQ/dK/dV kernel."""
+    import torch
+    from varlenabsorbflashattn_amd import workloads as W
+    return W.VarlenCase("varlen_fused_bwd_lq16", [16] * 64, [8192] * 64, 4, 64, torch.bfloat16)
+
+
+def fused_bwd_bytes(case):
+    """Algorithmic backward bytes: q, o, dO read and dq written per query row
+    (plus LSE), k, v read and dk, dv written per key row, 2-byte elements."""
+    Tq, Tk = sum(case.q_lens), sum(case.k_lens)
+    return float(case.H * case.D * 2 * (4 * Tq + 4 * Tk) + case.H * 4 * Tq)
 
 
 def bench_varlen_c3(iters):
@@ -414,6 +429,12 @@ def run_only(which, steps, warmup):
         return {"config": which, "ms_per_step": ms,
                 "TFLOP/s": (case.flops_fwd + case.flops_bwd) / (ms * 1e-3) / 1e12,
                 **varlen_line(case, step_st, fwd_st), "dkv_ms": dkv_st}
+    if which == "fused":
+        case = fused_case()
+        step_st, fwd_st = bench_varlen_case(case, max(steps, 3), warmup)
+        line = varlen_line(case, step_st, fwd_st)
+        line["bwd_GB/s"] = fused_bwd_bytes(case) / ((step_st["mean"] - fwd_st["mean"]) * 1e-3) / 1e9
+        return {"config": case.name, **line}
     if which == "d256":
         c = W.config2(seed=0)
         case = W.VarlenCase("c2_lengths_H8_D256", c.q_lens, c.k_lens, 8, 256, torch.bfloat16)
@@ -446,7 +467,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c5",
-                                       "d256", "copy", "replay"],
+                                       "d256", "fused", "copy", "replay"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -502,6 +523,14 @@ def main():
         s_st, f_st = bench_varlen_case(c2k, n2, 3)
         secondary["c2_varlen_fwd_bwd_128k_tokens"] = varlen_line(c2k, s_st, f_st)
         log("C2 at 128k tokens", s_st["mean"], f_st["mean"])
+        # decode-shaped training backward, where the fused key-major
+        # dQ/dK/dV path runs (16 queries per segment, D <= 64)
+        cf = fused_case()
+        s_st, f_st = bench_varlen_case(cf, n2, 3)
+        line = varlen_line(cf, s_st, f_st)
+        line["bwd_GB/s"] = fused_bwd_bytes(cf) / ((s_st["mean"] - f_st["mean"]) * 1e-3) / 1e9
+        secondary["varlen_fused_bwd_lq16_H4_D64"] = line
+        log("fused-path shape", s_st["mean"], f_st["mean"], line["bwd_GB/s"])
         # D=256 (fa/interface.py:167 accepts it) on C2's lengths at H=8
         c256 = W.VarlenCase("c2_lengths_H8_D256", case.q_lens, case.k_lens, 8, 256,
                             torch.bfloat16)

@@ -106,6 +106,17 @@ typedef struct vafa_plan_info {
   int64_t max_comb_rows;          /* most rows (tokens) of one combine item */
   int64_t n_kv_res;               /* absorb: the leading key-tile items whose
                                      segment has at most 64 (token, head) rows */
+  /* varlen backward: the dQ pass runs over the forward items of the
+   * segments that are not fused (dq, dqc: filtered copies of fwd, comb);
+   * fused segments (at most 16 queries, D <= 64) run dQ/dK/dV in one
+   * K-major pass over fkv items whose fp32 dQ partials fcomb sums. */
+  int64_t off_dq, n_dq;           /* dQ-pass items                          */
+  int64_t off_dqc, n_dqc;         /* dQ-pass combine items                  */
+  int64_t max_dqc_rows;
+  int64_t off_fkv, n_fkv;         /* fused key-tile items                   */
+  int64_t off_fcomb, n_fcomb;     /* fused dQ-partial sums                  */
+  int64_t n_fpart_rows;           /* fused dQ partial rows                  */
+  int64_t max_fcomb_rows;
 } vafa_plan_info;
 
 /* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).

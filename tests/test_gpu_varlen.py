@@ -34,6 +34,11 @@ CASES = [
     # half-wave row at D <= 32)
     ("many_splits_d64", [20, 3], [270000, 5000], 64),
     ("many_splits_d32", [20, 7], [140000, 900], 32),
+    # fused key-major backward (segments with 1..16 queries at D <= 64): its
+    # boundary, key tiles with idle waves (< 32 keys), both head dims it serves
+    ("fused_boundary", [16, 17, 1], [5000, 5000, 700], 64),
+    ("fused_short_keys", [12, 5, 3], [3, 130, 33], 64),
+    ("fused_d32", [16, 2, 40], [600, 4100, 70], 32),
 ]
 
 

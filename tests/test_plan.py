@@ -171,24 +171,57 @@ def check_varlen_plan(q_lens, k_lens, H=4, D=64):
         assert [b for b, _ in slots] == [pbase + s * R for s in range(ns)]
         used[pbase:pbase + ns * R] += 1
     assert (used == 1).all()
-    # 3) key tiles cover each key once and carry the segment's query range
+    # 3) key tiles (plain and fused) cover each key once and carry the
+    #    segment's query range; a segment is fused iff it has 1..16 queries,
+    #    at least one key and D <= 64, and then all of its key tiles are
+    #    fused items (a segment without keys stays on the dQ pass, which
+    #    writes its zero rows)
+    lq = np.diff(cq)
+    fused = (lq > 0) & (lq <= 16) & (np.diff(ck) >= 1) & (D <= 64)
+    fkv, fcomb = p.section("fkv"), p.section("fcomb")
     keys = np.zeros(int(ck[-1]), dtype=np.int64)
     for k0, k1, q0, q1, seg, *_ in kv.tolist():
-        assert (q0, q1) == (cq[seg], cq[seg + 1])
+        assert (q0, q1) == (cq[seg], cq[seg + 1]) and not fused[seg]
+        keys[k0:k1] += 1
+    for k0, k1, q0, q1, seg, *_ in fkv.tolist():
+        assert (q0, q1) == (cq[seg], cq[seg + 1]) and fused[seg]
         keys[k0:k1] += 1
     assert (keys == 1).all()
     # 4) longest-first order
     lens = (fwd[:, 3] - fwd[:, 2]).astype(np.int64)
     assert (np.diff(lens) <= 0).all()
+    # 5) the dQ pass runs the forward items (and combines) of the segments
+    #    that are not fused, in forward order
+    dq, dqc = p.section("dq"), p.section("dqc")
+    assert dq.tolist() == [r for r in fwd.tolist() if not fused[r[5]]]
+    assert dqc.tolist() == [r for r in comb.tolist() if not fused[r[4]]]
+    assert p.info.max_dqc_rows == max([r[1] - r[0] for r in dqc.tolist()], default=0)
+    # 6) fused partial rows: tile j of a segment writes rows pbase + j*Lq + r,
+    #    the tiles of all fused segments tile [0, n_fpart_rows) exactly once
+    assert sorted(r[4] for r in fcomb.tolist()) == [s for s in range(len(q_lens))
+                                                     if fused[s] and k_lens[s] > 0]
+    fused_used = np.zeros(p.info.n_fpart_rows, dtype=np.int64)
+    tiles = {}
+    for k0, k1, q0, q1, seg, pbase, j, nt in fkv.tolist():
+        assert k0 == ck[seg] + 128 * j and nt == -(-int(k_lens[seg]) // 128)
+        tiles.setdefault(seg, []).append((j, pbase))
+    for q0, q1, pbase, nt, seg, *_ in fcomb.tolist():
+        R = q1 - q0
+        assert sorted(tiles[seg]) == [(j, pbase + j * R) for j in range(nt)]
+        fused_used[pbase:pbase + nt * R] += 1
+    assert (fused_used == 1).all()
+    assert p.info.max_fcomb_rows == max([r[1] - r[0] for r in fcomb.tolist()], default=0)
     return p
 
 
 def test_varlen_plan_small_cases():
     cases = [([7, 11], [19, 5]), ([129, 257], [33, 130]), ([500, 500], [19, 800]),
              ([512, 512], [500, 500]), ([400], [400]), ([256, 256], [128, 128]),
-             ([0, 5, 0], [3, 0, 9]), ([300, 20], [9000, 70000]), ([16, 3], [32768, 1024])]
+             ([0, 5, 0], [3, 0, 9]), ([300, 20], [9000, 70000]), ([16, 3], [32768, 1024]),
+             ([16, 17, 1], [5000, 5000, 0]), ([64, 2], [129, 128])]
     for ql, kl in cases:
-        check_varlen_plan(ql, kl)
+        for D in (32, 64, 128, 256):
+            check_varlen_plan(ql, kl, D=D)
 
 
 def test_varlen_plan_split_counts_match_reference_rule():

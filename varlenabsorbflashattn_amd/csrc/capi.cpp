@@ -60,7 +60,7 @@ bool supported_d(int64_t D) {
 
 // ---- varlen ---------------------------------------------------------------
 struct VarlenWs {
-  float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr;
+  float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *part_fq = nullptr;
   int64_t bytes = 0;
 };
 
@@ -71,6 +71,7 @@ VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd)
   if (bwd) w.delta = c.take<float>(info->T_q * info->H * 4);
   w.part_o = c.take<float>(rows * D * 4);
   if (!bwd) w.part_lse = c.take<float>(rows * 4);
+  if (bwd) w.part_fq = c.take<float>(info->n_fpart_rows * info->H * D * 4);
   w.bytes = c.used;
   return w;
 }
@@ -98,25 +99,42 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
 
 // Backward stages.  Matrix-core kernels for D in {32, 64, 128, 256}; D=16
 // (below the 32-wide output tiles of the 32x32x16 products) and fp32 take the
-// wave-per-row kernels.
+// wave-per-row kernels.  Segments the plan fuses (few queries, D <= 64) run
+// dQ/dK/dV in the fused key-major kernel, whose dQ partials are summed in
+// order; without matrix cores their key tiles go to the plain dK/dV kernel
+// and their dQ to the dQ pass over every forward item.
 inline bool mfma_bwd_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
+template <typename T>
+bool fused_path(const VarlenArgs &a) {
+  return sizeof(T) == 2 && a.n_fkv > 0 && (a.D == 32 || a.D == 64);
+}
 
 template <typename T>
 void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
   const bool mfma = sizeof(T) == 2 && mfma_bwd_d(a.D);
+  const bool fq = fused_path<T>(a);
   if (stage == VAFA_BWD_DELTA) {
     launch_row_dot<T>(a.o_in, a.dout, a.delta, a.T_q * a.H, a.D, st);
   } else if (stage == VAFA_BWD_DQ) {
+    VarlenArgs d = a;
+    if (fq) {  // the fused kernel owns the fused segments' dQ
+      d.items = a.dq_items;
+      d.n_items = a.n_dq;
+      d.comb_items = a.dqc_items;
+      d.n_comb = a.n_dqc;
+      d.comb_rows = a.dqc_rows;
+    }
     if constexpr (sizeof(T) == 2) {
       if (mfma) {
-        if (a.D == 32) launch_mfma_varlen_dq<T, 32>(a, st);
-        if (a.D == 64) launch_mfma_varlen_dq<T, 64>(a, st);
-        if (a.D == 128) launch_mfma_varlen_dq<T, 128>(a, st);
-        if (a.D == 256) launch_mfma_varlen_dq<T, 256>(a, st);
+        if (a.D == 32) launch_mfma_varlen_dq<T, 32>(d, st);
+        if (a.D == 64) launch_mfma_varlen_dq<T, 64>(d, st);
+        if (a.D == 128) launch_mfma_varlen_dq<T, 128>(d, st);
+        if (a.D == 256) launch_mfma_varlen_dq<T, 256>(d, st);
       }
     }
-    if (!mfma) launch_simt_varlen_dq<T>(a, st);
-    launch_sum_combine<T>(a.part_o, a.dq, a.comb_items, a.n_comb, a.H, a.D, a.comb_rows, st);
+    if (!mfma) launch_simt_varlen_dq<T>(d, st);
+    launch_sum_combine<T>(d.part_o, d.dq, d.comb_items, d.n_comb, d.H, d.D, d.comb_rows, st);
   } else {
     if constexpr (sizeof(T) == 2) {
       if (mfma) {
@@ -125,19 +143,42 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
         if (a.D == 128) launch_mfma_varlen_dkv<T, 128>(a, st);
         if (a.D == 256) launch_mfma_varlen_dkv<T, 256>(a, st);
       }
+      if (fq) {
+        if (a.D == 32) launch_mfma_varlen_fkv<T, 32>(a, st);
+        if (a.D == 64) launch_mfma_varlen_fkv<T, 64>(a, st);
+        launch_sum_combine<T>(a.part_fq, a.dq, a.fcomb_items, a.n_fcomb, a.H, a.D, a.fcomb_rows,
+                              st);
+      }
     }
     if (!mfma) launch_simt_varlen_dkv<T>(a, st);
+    if (!fq && a.n_fkv > 0) {
+      // fused-planned key tiles on the plain dK/dV kernels ({k0, k1, q0, q1}
+      // leads both item formats)
+      VarlenArgs kv = a;
+      kv.kv_items = a.fkv_items;
+      kv.n_kv = a.n_fkv;
+      if constexpr (sizeof(T) == 2) {
+        if (mfma) {
+          if (a.D == 32) launch_mfma_varlen_dkv<T, 32>(kv, st);
+          if (a.D == 64) launch_mfma_varlen_dkv<T, 64>(kv, st);
+          if (a.D == 128) launch_mfma_varlen_dkv<T, 128>(kv, st);
+          if (a.D == 256) launch_mfma_varlen_dkv<T, 256>(kv, st);
+        }
+      }
+      if (!mfma) launch_simt_varlen_dkv<T>(kv, st);
+    }
   }
 }
 
 // All stages in order.  The matrix-core dQ kernel forms delta itself (the
-// same bits as the delta stage) and leaves it for dK/dV.
+// same bits as the delta stage) and leaves it for dK/dV -- unless fused
+// segments exist, whose rows it does not see: then the delta stage runs.
 template <typename T>
 void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
   const bool mfma = sizeof(T) == 2 && mfma_bwd_d(a.D);
   VarlenArgs f = a;
-  f.fuse_delta = mfma;
-  if (!mfma) varlen_bwd_stage<T>(VAFA_BWD_DELTA, f, st);
+  f.fuse_delta = mfma && !fused_path<T>(a);
+  if (!f.fuse_delta) varlen_bwd_stage<T>(VAFA_BWD_DELTA, f, st);
   varlen_bwd_stage<T>(VAFA_BWD_DQ, f, st);
   varlen_bwd_stage<T>(VAFA_BWD_DKV, f, st);
 }
@@ -345,7 +386,13 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   VarlenArgs a{};
   a.q = q; a.k = k; a.v = v; a.o_in = o; a.dout = dout; a.lse_in = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
-  a.delta = w.delta; a.part_o = w.part_o;
+  a.delta = w.delta; a.part_o = w.part_o; a.part_fq = w.part_fq;
+  a.dq_items = plan_dev + info->off_dq; a.n_dq = info->n_dq;
+  a.dqc_items = plan_dev + info->off_dqc; a.n_dqc = info->n_dqc;
+  a.dqc_rows = (int)info->max_dqc_rows;
+  a.fkv_items = plan_dev + info->off_fkv; a.n_fkv = info->n_fkv;
+  a.fcomb_items = plan_dev + info->off_fcomb; a.n_fcomb = info->n_fcomb;
+  a.fcomb_rows = (int)info->max_fcomb_rows;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.comb_rows = (int)info->max_comb_rows;

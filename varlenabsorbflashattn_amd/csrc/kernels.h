@@ -24,6 +24,12 @@ struct VarlenArgs {
   // the matrix-core dQ kernel computes delta from O and dO itself and writes
   // it for dK/dV (no separate row_dot launch)
   bool fuse_delta;
+  // backward: the dQ pass's items (forward items of the segments that are not
+  // fused) and the fused K-major pass (key tiles, partial-dQ sums)
+  const int32_t *dq_items, *dqc_items, *fkv_items, *fcomb_items;
+  int64_t n_dq, n_dqc, n_fkv, n_fcomb;
+  int dqc_rows, fcomb_rows;
+  float *part_fq;  // fused dQ partial rows [n_fpart_rows, H, D] fp32
 };
 
 struct AbsorbArgs {
@@ -81,6 +87,8 @@ void launch_absorb_dax(const AbsorbArgs &, hipStream_t);
 template <typename T, int D> void launch_mfma_varlen_fwd(const VarlenArgs &, hipStream_t);
 template <typename T, int D> void launch_mfma_varlen_dq(const VarlenArgs &, hipStream_t);
 template <typename T, int D> void launch_mfma_varlen_dkv(const VarlenArgs &, hipStream_t);
+// fused dQ/dK/dV over the fkv items (D <= 128): dK, dV and dQ partial rows
+template <typename T, int D> void launch_mfma_varlen_fkv(const VarlenArgs &, hipStream_t);
 
 // absorb_mfma.hip (bf16 / f16)
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);

@@ -116,28 +116,40 @@ std::vector<Item> xcd_bundle(const std::vector<Item> &items) {
   return out;
 }
 
-int emit(const std::vector<Item> &sec0, const std::vector<Item> &sec1,
-         const std::vector<Item> &sec2, const std::vector<Item> &sec3, int32_t *plan,
-         int64_t cap, vafa_plan_info *info) {
-  info->off_fwd = 0;
-  info->n_fwd = (int64_t)sec0.size();
-  info->off_comb = info->off_fwd + info->n_fwd * VAFA_ITEM_INTS;
-  info->n_comb = (int64_t)sec1.size();
-  // combine items start {q0, q1, ...} in both plans
-  info->max_comb_rows = 0;
-  for (const Item &it : sec1)
-    info->max_comb_rows = std::max<int64_t>(info->max_comb_rows, it.v[1] - it.v[0]);
-  info->off_kv = info->off_comb + info->n_comb * VAFA_ITEM_INTS;
-  info->n_kv = (int64_t)sec2.size();
-  info->off_qt = info->off_kv + info->n_kv * VAFA_ITEM_INTS;
-  info->n_qt = (int64_t)sec3.size();
-  info->plan_ints = info->off_qt + info->n_qt * VAFA_ITEM_INTS;
+int64_t max_rows(const std::vector<Item> &comb) {
+  // combine items start {q0, q1, ...} in every plan
+  int64_t m = 0;
+  for (const Item &it : comb) m = std::max<int64_t>(m, it.v[1] - it.v[0]);
+  return m;
+}
+
+// Lays the sections out back to back: fwd, comb, kv, qt, then the varlen
+// backward's dq, dqc, fkv, fcomb.
+int emit(const std::vector<Item> &fwd, const std::vector<Item> &comb,
+         const std::vector<Item> &kv, const std::vector<Item> &qt, const std::vector<Item> &dq,
+         const std::vector<Item> &dqc, const std::vector<Item> &fkv,
+         const std::vector<Item> &fcomb, int32_t *plan, int64_t cap, vafa_plan_info *info) {
+  const std::vector<Item> *secs[] = {&fwd, &comb, &kv, &qt, &dq, &dqc, &fkv, &fcomb};
+  int64_t *offs[] = {&info->off_fwd, &info->off_comb, &info->off_kv, &info->off_qt,
+                     &info->off_dq, &info->off_dqc, &info->off_fkv, &info->off_fcomb};
+  int64_t *counts[] = {&info->n_fwd, &info->n_comb, &info->n_kv, &info->n_qt,
+                       &info->n_dq, &info->n_dqc, &info->n_fkv, &info->n_fcomb};
+  int64_t off = 0;
+  for (int i = 0; i < 8; ++i) {
+    *offs[i] = off;
+    *counts[i] = (int64_t)secs[i]->size();
+    off += *counts[i] * VAFA_ITEM_INTS;
+  }
+  info->plan_ints = off;
+  info->max_comb_rows = max_rows(comb);
+  info->max_dqc_rows = max_rows(dqc);
+  info->max_fcomb_rows = max_rows(fcomb);
   if (plan == nullptr) return VAFA_OK;
   if (cap < info->plan_ints)
     return fail(VAFA_ERR_CAPACITY, "plan buffer holds %lld int32, %lld needed",
                 (long long)cap, (long long)info->plan_ints);
   int32_t *p = plan;
-  for (const auto *sec : {&sec0, &sec1, &sec2, &sec3})
+  for (const auto *sec : secs)
     for (const Item &it : *sec) {
       std::memcpy(p, it.v, sizeof(it.v));
       p += VAFA_ITEM_INTS;
@@ -251,7 +263,17 @@ int vafa_chunk_indices(const int64_t *cu, int64_t n1, int32_t BT, int32_t *out, 
 //   kv section    : one item per (segment, key tile) for dK/dV:
 //                   {k0, k1, q0, q1, seg, 0, 0, 0} with [q0,q1) the segment's
 //                   whole query range.
-// The dQ pass reuses the fwd and comb sections with its own partial buffer.
+//   dq, dqc       : the fwd and comb items of the segments that are not fused
+//                   (same order, same partial rows): the dQ pass, which reuses
+//                   the forward's split layout with its own partial buffer.
+//   fkv section   : fused segments (at most kFusedMaxQ queries, D <=
+//                   kFusedMaxD), one item per key tile:
+//                   {k0, k1, q0, q1, seg, pbase, tile, ntiles}; the tile's
+//                   scaled fp32 dQ partial of query q lands in row
+//                   pbase + (q - q0).
+//   fcomb section : one item per fused segment, {q0, q1, pbase, ntiles, seg,
+//                   0, 0, 0}: tile t of the segment owns rows
+//                   pbase + t*(q1-q0) + r (the comb layout), summed in order.
 int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H, int64_t D,
                      int32_t *plan, int64_t plan_cap, vafa_plan_info *info) {
   int rc = check_pair(cu_q, cu_k, n1);
@@ -267,13 +289,14 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   info->H = H;
   info->q_tile = BM;
   info->k_tile = BK;
-  (void)D;
-  std::vector<Item> fwd, comb, kv;
-  int64_t prow = 0;
+  std::vector<Item> fwd, comb, kv, fkv, fcomb;
+  std::vector<char> fused(n1 > 1 ? n1 - 1 : 0, 0);
+  int64_t prow = 0, fprow = 0;
   int64_t max_split = 1;
   for (int64_t s = 0; s + 1 < n1; ++s) {
     const int64_t q0 = cu_q[s], q1 = cu_q[s + 1], k0 = cu_k[s], k1 = cu_k[s + 1];
     const int64_t lq = q1 - q0, lk = k1 - k0;
+    fused[s] = lq > 0 && lq <= kFusedMaxQ && lk >= kFusedMinK && D <= kFusedMaxD;
     for (int64_t t = q0; t < q1; t += BM) {
       const int64_t te = std::min(t + BM, q1), rows = te - t;
       int64_t ns, chunk;
@@ -296,18 +319,36 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
       }
       prow += ns * rows;
     }
-    for (int64_t k = k0; k < k1; k += BK) {
+    const int64_t ntiles = (lk + BK - 1) / BK;
+    for (int64_t k = k0, j = 0; k < k1; k += BK, ++j) {
       const int64_t ke = std::min(k + BK, k1);
-      Item it{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s, 0, 0, 0},
-              lq + pol.item_overhead};
-      kv.push_back(it);
+      if (fused[s]) {
+        fkv.push_back(Item{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s,
+                            (int32_t)(fprow + j * lq), (int32_t)j, (int32_t)ntiles},
+                           lq + pol.item_overhead});
+      } else {
+        kv.push_back(Item{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s, 0, 0, 0},
+                          lq + pol.item_overhead});
+      }
+    }
+    if (fused[s] && ntiles > 0) {
+      fcomb.push_back(Item{{(int32_t)q0, (int32_t)q1, (int32_t)fprow, (int32_t)ntiles,
+                            (int32_t)s, 0, 0, 0}, 0});
+      fprow += ntiles * lq;
     }
   }
   sort_lpt(fwd);
   sort_lpt(kv);
+  sort_lpt(fkv);
+  std::vector<Item> dq, dqc;
+  for (const Item &it : fwd)
+    if (!fused[it.v[5]]) dq.push_back(it);
+  for (const Item &it : comb)
+    if (!fused[it.v[4]]) dqc.push_back(it);
   info->n_part_rows = prow;
+  info->n_fpart_rows = fprow;
   info->max_split = max_split;
-  return emit(fwd, comb, kv, {}, plan, plan_cap, info);
+  return emit(fwd, comb, kv, {}, dq, dqc, fkv, fcomb, plan, plan_cap, info);
 }
 
 // Absorb plan.  Query rows are (token, head) pairs; one item covers whole
@@ -409,7 +450,7 @@ int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   sort_lpt(qt);
   info->n_part_rows = prow;
   info->max_split = max_split;
-  return emit(fwd, comb, kv, qt, plan, plan_cap, info);
+  return emit(fwd, comb, kv, qt, {}, {}, {}, {}, plan, plan_cap, info);
 }
 
 }  // extern "C"

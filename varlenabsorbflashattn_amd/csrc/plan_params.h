@@ -37,6 +37,21 @@ constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 1024, 1024, 64, 32}
 constexpr int64_t kAbsorbSlots = 768;
 constexpr int64_t kAbsorbSplitSlack = 3;
 
+// Varlen backward, fused K-major path (dQ, dK, dV in one kernel per 128-key
+// tile, fp32 dQ partials per tile summed in order): segments with at most
+// kFusedMaxQ queries and at least kFusedMinK keys, at head dims up to
+// kFusedMaxD.  Each tile writes Lq*D*4 bytes of partial dQ (plus the read back
+// in the sum) and saves the second read of its K/V rows that the query-major
+// dQ kernel makes.  Measured on the MI355X (64 segments x 8192 keys, backward
+// ms, two-kernel vs fused): H=4 D=64 Lq=1/8/16: 0.447/0.440/0.451 vs
+// 0.379/0.387/0.394; Lq=32 0.443 vs 0.440; Lq=48/64 0.487/0.472 vs
+// 0.519/0.561.  At D=128 the fused kernel holds one workgroup per CU (256
+// VGPRs + 225 AGPRs, 117 KB of LDS) and lost at every Lq (1.57-1.59 vs
+// 1.65-1.95 ms at H=8), so it serves D <= 64 only.
+constexpr int kFusedMaxQ = 16;
+constexpr int kFusedMinK = 1;
+constexpr int kFusedMaxD = 64;
+
 // Workgroups are dispatched round-robin over this many XCDs (one L2 each):
 // workgroup i runs on XCD i % kXcds.
 constexpr int kXcds = 8;

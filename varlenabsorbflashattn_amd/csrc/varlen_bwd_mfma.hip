@@ -11,6 +11,12 @@
 //       dV^T += dO^T P,  dK^T += Q^T dS           (4 products per block)
 //   * dQ, query-major over the forward's plan items (including split-K
 //     partials): S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+//   * fused dQ/dK/dV, key-major (segments with few queries): the dK/dV kernel
+//     with FQ = true also forms dQ^T = K^T dS^T for its 128 keys per query
+//     block (dS^T through LDS, K^T operands read once, transposed, from the
+//     wave's K rows), sums the four waves' contributions in a fixed order and
+//     writes scaled fp32 partial rows, one set per key tile, that an ordered
+//     sum turns into dQ (the dead template of fa/kernels.py:923-1099).
 // The dQ kernel stages K / V blocks through registers.  Its row statistics stay
 // per lane (lane <-> query row); the dK/dV kernel reads LSE and delta of its
 // 32-row block from LDS.  LDS operands are read a few products ahead of the
@@ -35,6 +41,22 @@ struct DkvSmem {
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
+// Extra LDS of the fused variant, after DkvSmem: region R holds first the
+// waves' K rows (staged once for the transposed K^T reads) and then, per query
+// block, the four waves' dQ^T contributions [wave][q][D + 4] fp32; then one
+// [32 keys][40] dS^T tile per wave.
+template <int D>
+struct FqSmem {
+  static constexpr int kKtBytes = 4 * 32 * DkvSmem<D>::RS * 2;
+  static constexpr int kRS = D + 4;
+  static constexpr int kRedBytes = 4 * 32 * kRS * 4;
+  static constexpr int kROff = DkvSmem<D>::kBytes;
+  static constexpr int kRBytes = kKtBytes > kRedBytes ? kKtBytes : kRedBytes;
+  static constexpr int kDsS = 40;
+  static constexpr int kDsOff = kROff + kRBytes;
+  static constexpr int kBytes = kDsOff + 4 * 32 * kDsS * 2;
+};
+
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
 // past r_end read as zero) into a padded [32][RS] block: wave w moves rows
 // 8w .. 8w+7, one instruction per row with lanes < D/8 active.  One buffer
@@ -57,12 +79,12 @@ __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H,
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool FQ>
 __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
-    float scale) {
+    float scale, float *__restrict__ part_dq) {
   using M = Mfma<T>;
   using S = DkvSmem<D>;
   constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
@@ -110,6 +132,22 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       vf[cc] = as_v8<T>(b);
     }
   }
+  // fused: the A operands of dQ^T = K^T dS^T (loop-invariant), read
+  // transposed from the wave's own K rows staged in LDS region R
+  typename M::v8 ktf[FQ ? 2 * ND : 1];
+  if constexpr (FQ) {
+    if (wave_active) {
+      T *kt = reinterpret_cast<T *>(smem_raw + FqSmem<D>::kROff) + wave * 32 * RS;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+        *reinterpret_cast<typename M::v8 *>(kt + lrow * RS + cc * 16 + lhalf * 8) = kf[cc];
+#pragma unroll
+      for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) ktf[hk * ND + dt] = tr_operand<T>(kt, RS, 16 * hk, 32 * dt, lane);
+    }
+  }
+  const int pbase = FQ ? it.v[5] : 0;
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i)
@@ -125,107 +163,170 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     wait_vmcnt<0>();
     __syncthreads();  // block j visible; every wave is done with the other buffer
     if (j + 1 < nblk) issue(q0 + (j + 1) * kRB, (j + 1) & 1);
-    if (!wave_active) continue;
-    const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
-    const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
-    const lds_cptr<T> ds_ = qs + S::kQs;
-    const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
-    // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
-    auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
-    f32x16 s, dp;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-    u32x4 ring[kPre];
-#pragma unroll
-    for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
-      const typename M::v8 a = as_v8<T>(ring[i % kPre]);
-      if (i & 1)
-        dp = M::mma(a, vf[i >> 1], dp);
-      else
-        s = M::mma(a, kf[i >> 1], s);
-      if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+    if (wave_active) {
+      const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
+      const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
+      const lds_cptr<T> ds_ = qs + S::kQs;
+      const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
+      // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
+      auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
+      f32x16 s, dp;
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+      u32x4 ring[kPre];
+  #pragma unroll
+      for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    // transposed operands: i -> d tile i % ND, query half mm = (i / ND) >> 1,
-    // dO^T (for dV^T, with P) when (i / ND) is even, else Q^T (for dK^T, with dS)
-    auto top = [&](int i) {
-      const lds_cptr<T> p =
-          (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
-      return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
-    };
-    typename M::v8 tring[kPre];
-#pragma unroll
-    for (int i = 0; i < kPre; ++i) tring[i] = top(i);
-    // P = exp2(S*c - LSE) and dS = P (dP - delta) per accumulator row r
-    // (query 8*(r/4) + 4*lhalf + r%4 of the block); keys past k1 have zero K
-    // and V rows, their dK / dV columns are never stored, so their P needs no
-    // masking.
-    typename M::v8 pb[2], sb[2];
-    // rows 0..7 (first 16 queries) before the products; rows 8..15 are
-    // computed under the first half of the chain, which only reads rows 0..7,
-    // their LSE / delta read one product ahead
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
-      const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = g * 4 + e;
-        const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
-        s[r] = p;
-        dp[r] = p * (dp[r] - Dl[e]);
+  #pragma unroll
+      for (int i = 0; i < 2 * NC; ++i) {
+        const typename M::v8 a = as_v8<T>(ring[i % kPre]);
+        if (i & 1)
+          dp = M::mma(a, vf[i >> 1], dp);
+        else
+          s = M::mma(a, kf[i >> 1], s);
+        if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    pb[0] = pack8<T>(s, 0);
-    sb[0] = pack8<T>(dp, 0);
-    // the 8 second-half rows are spread over the first 2*ND products: kRowsPer
-    // rows at every kEvery-th product (one row every second product at D=256)
-    constexpr int kSteps = 2 * ND < 8 ? 2 * ND : 8;
-    constexpr int kRowsPer = 8 / kSteps;
-    constexpr int kEvery = 2 * ND / kSteps;
-    auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
-    auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
-    float Ln[kRowsPer], Dn[kRowsPer];
-#pragma unroll
-    for (int rr = 0; rr < kRowsPer; ++rr) Ln[rr] = lse_at(8 + rr), Dn[rr] = del_at(8 + rr);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 4 * ND; ++i) {
-      const int dt = i % ND, q2 = i / ND, mm = q2 >> 1;
-      const typename M::v8 a = tring[i % kPre];
-      if (q2 & 1)
-        adk[dt] = M::mma(a, sb[mm], adk[dt]);
-      else
-        adv[dt] = M::mma(a, pb[mm], adv[dt]);
-      if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
-      if (i < 2 * ND && i % kEvery == 0) {
-        const int g = i / kEvery;
-        float Lc[kRowsPer], Dc[kRowsPer];
-#pragma unroll
-        for (int rr = 0; rr < kRowsPer; ++rr) {
-          Lc[rr] = Ln[rr], Dc[rr] = Dn[rr];
-          if (g + 1 < kSteps) {
-            const int rn = 8 + (g + 1) * kRowsPer + rr;
-            Ln[rr] = lse_at(rn);
-            Dn[rr] = del_at(rn);
+      // transposed operands: i -> d tile i % ND, query half mm = (i / ND) >> 1,
+      // dO^T (for dV^T, with P) when (i / ND) is even, else Q^T (for dK^T, with dS)
+      auto top = [&](int i) {
+        const lds_cptr<T> p =
+            (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
+        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+      };
+      typename M::v8 tring[kPre];
+  #pragma unroll
+      for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+      // P = exp2(S*c - LSE) and dS = P (dP - delta) per accumulator row r
+      // (query 8*(r/4) + 4*lhalf + r%4 of the block); keys past k1 have zero K
+      // and V rows, their dK / dV columns are never stored, so their P needs no
+      // masking.
+      typename M::v8 pb[2], sb[2];
+      // rows 0..7 (first 16 queries) before the products; rows 8..15 are
+      // computed under the first half of the chain, which only reads rows 0..7,
+      // their LSE / delta read one product ahead
+  #pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
+        const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = g * 4 + e;
+          const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
+          s[r] = p;
+          dp[r] = p * (dp[r] - Dl[e]);
+        }
+      }
+      pb[0] = pack8<T>(s, 0);
+      sb[0] = pack8<T>(dp, 0);
+      // the 8 second-half rows are spread over the first 2*ND products: kRowsPer
+      // rows at every kEvery-th product (one row every second product at D=256)
+      constexpr int kSteps = 2 * ND < 8 ? 2 * ND : 8;
+      constexpr int kRowsPer = 8 / kSteps;
+      constexpr int kEvery = 2 * ND / kSteps;
+      auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
+      auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
+      float Ln[kRowsPer], Dn[kRowsPer];
+  #pragma unroll
+      for (int rr = 0; rr < kRowsPer; ++rr) Ln[rr] = lse_at(8 + rr), Dn[rr] = del_at(8 + rr);
+      __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+      for (int i = 0; i < 4 * ND; ++i) {
+        const int dt = i % ND, q2 = i / ND, mm = q2 >> 1;
+        const typename M::v8 a = tring[i % kPre];
+        if (q2 & 1)
+          adk[dt] = M::mma(a, sb[mm], adk[dt]);
+        else
+          adv[dt] = M::mma(a, pb[mm], adv[dt]);
+        if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
+        if (i < 2 * ND && i % kEvery == 0) {
+          const int g = i / kEvery;
+          float Lc[kRowsPer], Dc[kRowsPer];
+  #pragma unroll
+          for (int rr = 0; rr < kRowsPer; ++rr) {
+            Lc[rr] = Ln[rr], Dc[rr] = Dn[rr];
+            if (g + 1 < kSteps) {
+              const int rn = 8 + (g + 1) * kRowsPer + rr;
+              Ln[rr] = lse_at(rn);
+              Dn[rr] = del_at(rn);
+            }
+          }
+  #pragma unroll
+          for (int rr = 0; rr < kRowsPer; ++rr) {
+            const int r = 8 + g * kRowsPer + rr;
+            const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lc[rr]));
+            s[r] = p;
+            dp[r] = p * (dp[r] - Dc[rr]);
+          }
+          if (g == kSteps - 1) {
+            pb[1] = pack8<T>(s, 8);
+            sb[1] = pack8<T>(dp, 8);
           }
         }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (FQ) {
+        // dS of this lane (key lrow; queries 8*(r/4) + 4*lhalf + r%4) to LDS
+        // as dS^T [key][query], rounded to T as for dK
+        T *dst = reinterpret_cast<T *>(smem_raw + FqSmem<D>::kDsOff) + wave * 32 * FqSmem<D>::kDsS;
+        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
 #pragma unroll
-        for (int rr = 0; rr < kRowsPer; ++rr) {
-          const int r = 8 + g * kRowsPer + rr;
-          const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lc[rr]));
-          s[r] = p;
-          dp[r] = p * (dp[r] - Dc[rr]);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          T4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(dp[4 * r4 + e]);
+          *reinterpret_cast<T4 *>(dst + lrow * FqSmem<D>::kDsS + 8 * r4 + 4 * lhalf) = w;
         }
-        if (g == kSteps - 1) {
-          pb[1] = pack8<T>(s, 8);
-          sb[1] = pack8<T>(dp, 8);
+        // dQ^T (D x 32 queries) = K^T dS^T over the wave's 32 keys; the
+        // dS^T operand is read transposed in the key order of the K^T reads
+        f32x16 dqa[ND];
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dqa[dt][r] = 0.f;
+#pragma unroll
+        for (int hk = 0; hk < 2; ++hk) {
+          const typename M::v8 b = tr_operand<T>(dst, FqSmem<D>::kDsS, 16 * hk, 0, lane);
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) dqa[dt] = M::mma(ktf[hk * ND + dt], b, dqa[dt]);
+        }
+        // this wave's rows [query][d] of the reduction region
+        float *red = reinterpret_cast<float *>(smem_raw + FqSmem<D>::kROff) +
+                     wave * 32 * FqSmem<D>::kRS;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            f32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = dqa[dt][4 * r4 + e];
+            *reinterpret_cast<f32x4 *>(red + lrow * FqSmem<D>::kRS + 32 * dt + 8 * r4 +
+                                       4 * lhalf) = w;
+          }
+      }
+    }
+    if constexpr (FQ) {
+      // ordered sum of the active waves' dQ^T rows, scaled: this key tile's
+      // partial dQ rows of the block's queries (the next iteration's barrier
+      // orders these reads before the region is written again)
+      __syncthreads();
+      const int nact = (k1 - k0 + 31) / 32 < 4 ? (k1 - k0 + 31) / 32 : 4;
+      const int row = tid >> 3, cs = tid & 7;  // 32 rows x 8 column segments
+      const int qb = q0 + j * kRB;
+      if (qb + row < q1) {
+        const float *red = reinterpret_cast<const float *>(smem_raw + FqSmem<D>::kROff);
+        float *prow = part_dq + ((int64_t)(pbase + qb - q0 + row) * H + h) * D;
+#pragma unroll
+        for (int c4 = 0; c4 < D / 32; ++c4) {
+          const int col = cs * (D / 8) + 4 * c4;
+          f32x4 acc = *reinterpret_cast<const f32x4 *>(red + row * FqSmem<D>::kRS + col);
+          for (int w = 1; w < nact; ++w)
+            acc += *reinterpret_cast<const f32x4 *>(red + (w * 32 + row) * FqSmem<D>::kRS + col);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] *= scale;
+          *reinterpret_cast<f32x4 *>(prow + col) = acc;
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
   wait_vmcnt<0>();
@@ -482,12 +583,24 @@ template <typename T, int D>
 void launch_mfma_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
   const int smem = DkvSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D>),
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, false>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D>), dim3((unsigned)(a.n_kv * a.H)), dim3(256), smem,
-                     st, (const T *)a.q, (const T *)a.k, (const T *)a.v, (const T *)a.dout,
-                     a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H, a.scale * kLog2e,
-                     a.scale);
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false>), dim3((unsigned)(a.n_kv * a.H)), dim3(256),
+                     smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
+                     (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
+                     a.scale * kLog2e, a.scale, nullptr);
+}
+
+template <typename T, int D>
+void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
+  if (a.n_fkv == 0) return;
+  const int smem = FqSmem<D>::kBytes;
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, true>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, true>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
+                     smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
+                     (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.fkv_items, a.H,
+                     a.scale * kLog2e, a.scale, a.part_fq);
 }
 
 template <typename T, int D>
@@ -506,6 +619,8 @@ void launch_mfma_varlen_dq(const VarlenArgs &a, hipStream_t st) {
 #define VAFA_INST(T, D)                                                           \
   template void launch_mfma_varlen_dkv<T, D>(const VarlenArgs &, hipStream_t);    \
   template void launch_mfma_varlen_dq<T, D>(const VarlenArgs &, hipStream_t);
+#define VAFA_INST_F(T, D) \
+  template void launch_mfma_varlen_fkv<T, D>(const VarlenArgs &, hipStream_t);
 VAFA_INST(bf16, 32)
 VAFA_INST(bf16, 64)
 VAFA_INST(bf16, 128)
@@ -514,6 +629,11 @@ VAFA_INST(f16, 64)
 VAFA_INST(f16, 128)
 VAFA_INST(bf16, 256)
 VAFA_INST(f16, 256)
+VAFA_INST_F(bf16, 32)
+VAFA_INST_F(bf16, 64)
+VAFA_INST_F(f16, 32)
+VAFA_INST_F(f16, 64)
 #undef VAFA_INST
+#undef VAFA_INST_F
 
 }  // namespace vafa

@@ -12,7 +12,7 @@ and max over its timed iterations, each bracketed by HIP events (the
 reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c5,d256,fused,copy,replay}
+       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d256,fused,copy,replay}
 """
 from __future__ import annotations
 
@@ -446,6 +446,31 @@ def run_only(which, steps, warmup):
                 "GB/s": case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9}
     if which == "replay":
         return bench_replay(max(steps, 1), warmup)
+    if which == "c4full":
+        # the whole packed_target_attn (u projection included), fwd and fwd+bwd
+        from varlenabsorbflashattn_amd import packed_target_attn
+        case = W.config4(seed=0)
+        q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case)
+        ins = [t.detach().clone().requires_grad_(True) for t in (q_raw, X, W_Q, W_K, W_V)]
+        g = torch.Generator().manual_seed(1)
+        dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(u.device, u.dtype)
+
+        def call():
+            return packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck, q_chunk_indices=qi,
+                                      k_chunk_indices=ki, validate=False)
+
+        def step():
+            call().backward(dO)
+            for t in ins:
+                t.grad = None
+
+        def fwd():
+            with torch.no_grad():
+                call()
+
+        st = timed(step, max(steps, 1))
+        f_st = timed(fwd, max(steps, 1))
+        return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st}
     if which in ("c4b", "c4_fp32"):
         case = W.config4(seed=0)
         dt = torch.float32 if which == "c4_fp32" else None
@@ -466,7 +491,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
-    ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c5",
+    ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c4full", "c5",
                                        "d256", "fused", "copy", "replay"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()

@@ -218,11 +218,42 @@ VAFA_API int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, cons
  * torch einsum (ta/interface.py:434-435, 'thd,khd->thk'):
  * u[t,h,f] = sum_d q_proj[t, h*D_H + d] * W_K[f,h,d] with q_proj [T_q, H*D_H],
  * W_K [D_KV,H,D_H] -> u [T_q,H,D_KV], all in the given 16-bit dtype (fp32
- * accumulation, one rounding).  D_KV a multiple of 8, D_H a multiple of 16
- * up to 128; other shapes and fp32 return VAFA_ERR_VALUE. */
+ * accumulation, one rounding).  D_KV and D_H positive multiples of 8,
+ * 16-byte aligned operands; other shapes and fp32 return VAFA_ERR_VALUE. */
 VAFA_API int vafa_absorb_project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q,
                                    int64_t H, int64_t D_KV, int64_t D_H, int32_t dtype,
                                    void *stream);
+
+/* Workspace bytes of vafa_absorb_project_fwd (backward = 0) or
+ * vafa_absorb_project_bwd (backward = 1); -1 for unsupported dimensions. */
+VAFA_API int64_t vafa_absorb_project_workspace(int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV,
+                                               int64_t D_H, int32_t backward);
+
+/* Both projections of packed_target_attn (ta/interface.py:434-435):
+ * q_proj [T_q, H*D_H] = q_raw [T_q, D_Q] . W_Q [D_Q, H*D_H] and
+ * u [T_q, H, D_KV] = per head q_proj W_K[:,h,:]^T, each rounded once to the
+ * 16-bit dtype (as the reference's two 16-bit GEMMs).  q_proj is written for
+ * the backward.  D_Q, D_KV, D_H positive multiples of 8, 16-byte aligned
+ * operands and workspace. */
+VAFA_API int vafa_absorb_project_fwd(const void *q_raw, const void *W_Q, const void *W_K,
+                                     void *q_proj, void *u, int64_t T_q, int64_t H, int64_t D_Q,
+                                     int64_t D_KV, int64_t D_H, int32_t dtype, void *workspace,
+                                     int64_t workspace_bytes, void *stream);
+
+/* Backward of the projections, which the reference leaves to torch autograd
+ * (ta/interface.py:430-435): from du [T_q, H, D_KV],
+ *   dq_proj = per head du W_K[:,h,:]     (rounded, kept in the workspace)
+ *   dq_raw  = dq_proj W_Q^T              [T_q, D_Q]
+ *   dW_Q    = q_raw^T dq_proj            [D_Q, H, D_H]
+ *   dW_K    = per head du^T q_proj       [D_KV, H, D_H]
+ * Any of dq_raw, dW_Q, dW_K may be NULL (not computed).  The weight
+ * gradients are deterministic: fp32 partials over fixed token chunks summed
+ * in chunk order. */
+VAFA_API int vafa_absorb_project_bwd(const void *q_raw, const void *W_Q, const void *W_K,
+                                     const void *q_proj, const void *du, void *dq_raw,
+                                     void *dW_Q, void *dW_K, int64_t T_q, int64_t H, int64_t D_Q,
+                                     int64_t D_KV, int64_t D_H, int32_t dtype, void *workspace,
+                                     int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -270,20 +270,125 @@ def test_absorb_bf16_flag_3d_inputs_and_seqinfo(device):
     assert torch.equal(seqinfo, base)
 
 
+def _lib_call(fn, *args):
+    from varlenabsorbflashattn_amd import _lib
+    _lib.check(getattr(_lib.lib(), fn)(*args))
+
+
 @pytest.mark.parametrize("T,d_kv,H,D_H", [(9424, 256, 8, 32), (37, 216, 8, 32), (100, 64, 2, 16),
-                                          (70, 192, 4, 128), (5, 128, 1, 64)])
+                                          (70, 192, 4, 128), (5, 128, 1, 64), (45, 40, 3, 8),
+                                          (33, 64, 2, 256)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_project_u_kernel(device, T, d_kv, H, D_H, dtype):
     """vafa_absorb_project_u (the head einsum of ta/interface.py:435 on matrix
     cores) against a float64 einsum of the same 16-bit inputs: within one
     rounding to the output dtype, token-major [T, H, d_kv] layout."""
-    from varlenabsorbflashattn_amd.absorb import _HeadProject
+    from varlenabsorbflashattn_amd import _lib
     g = torch.Generator().manual_seed(T + d_kv)
     q_proj = torch.randn(T, H * D_H, generator=g).to(dtype)
     W_K = (torch.randn(d_kv, H, D_H, generator=g) * 0.2).to(dtype)
-    u = _HeadProject.apply(q_proj.to(device), W_K.to(device)).cpu()
+    qd, wd = q_proj.to(device), W_K.to(device)
+    u = torch.empty(T, H, d_kv, dtype=dtype, device=device)
+    _lib_call("vafa_absorb_project_u", qd.data_ptr(), wd.data_ptr(), u.data_ptr(), T, H, d_kv,
+              D_H, _lib.dtype_code(dtype), _lib.stream_ptr(device))
+    u = u.cpu()
     ref = torch.einsum("thk,jhk->thj", q_proj.double().view(T, H, D_H), W_K.double())
-    assert u.shape == (T, H, d_kv) and u.dtype == dtype
     err = (u.double() - ref).abs()
     bound = ref.abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-6
     assert (err <= bound).all(), float((err - bound).max())
+
+
+def _round_bound(ref, absprod, dtype, ulps_in=0.0):
+    """|got - ref| allowed for one rounding of a sum to ``dtype`` after fp32
+    accumulation: half an output ulp (taken as a relative 2^-8 / 2^-11, with
+    a factor 2 of slack), fp32 accumulation error (2^-16 of sum |a_k b_k|: a
+    few hundred fp32 additions per output at most, chunk partials included) and,
+    where an operand was itself a rounded product, ``ulps_in`` of its ulps
+    times sum |a_k b_k|."""
+    u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    return 2 * u * ref.abs() + (2.0 ** -16 + ulps_in * 2 * u) * absprod + 1e-30
+
+
+PROJECT_SHAPES = [(9424, 256, 256, 8, 32), (37, 968, 216, 8, 32), (1, 96, 64, 2, 16),
+                  (130, 40, 192, 4, 128), (0, 64, 64, 2, 32), (300, 72, 8, 3, 8)]
+
+
+@pytest.mark.parametrize("T,d_q,d_kv,H,D_H", PROJECT_SHAPES,
+                         ids=[f"T{s[0]}_dq{s[1]}_dkv{s[2]}_H{s[3]}_DH{s[4]}" for s in PROJECT_SHAPES])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_project_fwd_bwd_kernels(device, T, d_q, d_kv, H, D_H, dtype):
+    """vafa_absorb_project_fwd / _bwd through the C ABI against float64
+    products of the same 16-bit operands, each product rounded once as the
+    reference's 16-bit GEMMs (ta/interface.py:434-435 and torch autograd of
+    them): q_proj, u (from the kernel's own q_proj), dq_raw (from the rounded
+    float64 dq_proj = du W_K), dW_Q, dW_K; the backward twice with the same
+    inputs is bit-identical (deterministic weight gradients)."""
+    from varlenabsorbflashattn_amd import _lib
+    print(f"[project] T={T} d_q={d_q} d_kv={d_kv} H={H} D_H={D_H} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(T * 7 + d_q)
+    q_raw = torch.randn(T, d_q, generator=g).to(dtype)
+    W_Q = (torch.randn(d_q, H, D_H, generator=g) / math.sqrt(d_q)).to(dtype)
+    W_K = (torch.randn(d_kv, H, D_H, generator=g) / math.sqrt(d_kv)).to(dtype)
+    du = torch.randn(T, H, d_kv, generator=g).to(dtype)
+    HD = H * D_H
+    L = _lib.lib()
+    code, st = _lib.dtype_code(dtype), _lib.stream_ptr(device)
+    qd, wqd, wkd, dud = (t.to(device) for t in (q_raw, W_Q, W_K, du))
+    q_proj = torch.empty(T, HD, dtype=dtype, device=device)
+    u = torch.empty(T, H, d_kv, dtype=dtype, device=device)
+    ws = torch.empty(L.vafa_absorb_project_workspace(T, H, d_q, d_kv, D_H, 0), dtype=torch.uint8,
+                     device=device)
+    _lib_call("vafa_absorb_project_fwd", qd.data_ptr(), wqd.data_ptr(), wkd.data_ptr(),
+              q_proj.data_ptr(), u.data_ptr(), T, H, d_q, d_kv, D_H, code, ws.data_ptr(),
+              ws.numel(), st)
+    wsb = torch.empty(L.vafa_absorb_project_workspace(T, H, d_q, d_kv, D_H, 1),
+                      dtype=torch.uint8, device=device)
+    outs = []
+    for _ in range(2):
+        dq = torch.full((T, d_q), float("nan"), dtype=dtype, device=device)
+        dwq = torch.full((d_q, H, D_H), float("nan"), dtype=dtype, device=device)
+        dwk = torch.full((d_kv, H, D_H), float("nan"), dtype=dtype, device=device)
+        _lib_call("vafa_absorb_project_bwd", qd.data_ptr(), wqd.data_ptr(), wkd.data_ptr(),
+                  q_proj.data_ptr(), dud.data_ptr(), dq.data_ptr(), dwq.data_ptr(),
+                  dwk.data_ptr(), T, H, d_q, d_kv, D_H, code, wsb.data_ptr(), wsb.numel(), st)
+        outs.append([t.cpu() for t in (dq, dwq, dwk)])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    dq, dwq, dwk = outs[0]
+    q_proj, u = q_proj.cpu(), u.cpu()
+
+    d = torch.float64
+    qr, wq, wk, dd = q_raw.to(d), W_Q.to(d).reshape(d_q, HD), W_K.to(d), du.to(d)
+    checks = []
+    ref = qr @ wq
+    checks.append(("q_proj", q_proj, ref, qr.abs() @ wq.abs(), 0.0))
+    qp = q_proj.to(d).view(T, H, D_H)
+    ref = torch.einsum("thd,fhd->thf", qp, wk)
+    checks.append(("u", u, ref, torch.einsum("thd,fhd->thf", qp.abs(), wk.abs()), 0.0))
+    dqp = torch.einsum("thf,fhd->thd", dd, wk).reshape(T, HD)
+    dqp_abs = torch.einsum("thf,fhd->thd", dd.abs(), wk.abs()).reshape(T, HD)
+    dqp_r = dqp.to(dtype).to(d)
+    checks.append(("dq_raw", dq, dqp_r @ wq.t(), dqp_r.abs() @ wq.abs().t(), 1.0))
+    checks.append(("dW_Q", dwq.reshape(d_q, HD), qr.t() @ dqp_r, qr.abs().t() @ dqp_abs, 1.0))
+    ref = torch.einsum("thf,thd->fhd", dd, qp)
+    checks.append(("dW_K", dwk, ref, torch.einsum("thf,thd->fhd", dd.abs(), qp.abs()), 0.0))
+    for name, got, ref, absprod, ulps in checks:
+        assert got.shape == ref.shape, name
+        err = (got.to(d) - ref).abs()
+        bound = _round_bound(ref, absprod, dtype, ulps)
+        assert torch.isfinite(got).all() and (err <= bound).all(), \
+            (name, float((err - bound).max()), float(err.max()))
+
+
+def test_project_rejects_bad_shapes(device):
+    """Unsupported widths and dtypes return an error, and nothing runs."""
+    from varlenabsorbflashattn_amd import _lib
+    L = _lib.lib()
+    assert L.vafa_absorb_project_workspace(16, 2, 60, 64, 32, 0) == -1   # D_Q % 8
+    assert L.vafa_absorb_project_workspace(16, 2, 64, 64, 12, 1) == -1   # D_H % 8
+    x = torch.zeros(64, dtype=torch.float32, device=device)
+    rc = L.vafa_absorb_project_fwd(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                                   x.data_ptr(), 1, 1, 8, 8, 8, _lib.dtype_code(torch.float32),
+                                   x.data_ptr(), 256, _lib.stream_ptr(device))
+    assert rc != 0 and "16-bit" in _lib.last_error()

@@ -75,6 +75,11 @@ _SIGS = {
     "vafa_varlen_bwd_stage": (C.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _PINFO, _I64,
                                         _I32, C.c_float, _P, _I64, _P]),
     "vafa_absorb_project_u": (C.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
+    "vafa_absorb_project_workspace": (C.c_int64, [_I64, _I64, _I64, _I64, _I64, _I32]),
+    "vafa_absorb_project_fwd": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32,
+                                          _P, _I64, _P]),
+    "vafa_absorb_project_bwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                          _I64, _I32, _P, _I64, _P]),
     "vafa_absorb_fwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _PINFO, _I64, _I64, _I32, C.c_float,
                                   _P, _I64, _P]),
     "vafa_absorb_bwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _PINFO, _I64, _I64,

@@ -232,68 +232,87 @@ def target_attn_inner(
         q_chunk_indices, k_chunk_indices, validate)
 
 
-class _HeadProject(torch.autograd.Function):
-    """u[t,h,:] = q_proj[t,h,:] W_K[:,h,:]^T for every head (the einsum of
-    ta/interface.py:435).
+def _project_native(q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> bool:
+    """Whether ``vafa_absorb_project_fwd/_bwd`` take these operands: CUDA,
+    one 16-bit dtype, D_Q, D_KV and D_H multiples of 8."""
+    d_q = q_raw.shape[1]
+    d_kv, _, D_H = W_K.shape
+    return (q_raw.is_cuda and q_raw.dtype in (torch.bfloat16, torch.float16)
+            and W_Q.dtype == q_raw.dtype and W_K.dtype == q_raw.dtype
+            and d_q % 8 == 0 and d_kv % 8 == 0 and D_H % 8 == 0)
 
-    Forward: for 16-bit inputs, ``vafa_absorb_project_u`` (per-head products
-    on matrix cores, u written token-major ``[T, H, d_kv]``, fp32 sums rounded
-    once).  Otherwise ONE GEMM of q_proj ``[T, H*D_H]`` against the
-    block-diagonal ``[H*D_H, H*d_kv]`` matrix of the W_K[:,h,:]^T blocks, which
-    also writes u token-major -- no per-head outputs and no stacking copy.  For
-    finite q_proj the zero blocks add exact zeros to each fp32 sum, so every u
-    element is the same sum of products as per head (an infinite q_proj
-    element would spread NaN to the other heads' columns through 0 * inf).
-    Backward: per head on strided views (plain
-    2-D GEMMs, no batched products), so the zero blocks cost nothing there:
-    dq_proj[:,h,:] = du[:,h,:] W_K[:,h,:],  dW_K[:,h,:] = du[:,h,:]^T q_proj[:,h,:].
-    """
+
+class _Project(torch.autograd.Function):
+    """q_proj = q_raw W_Q, u[t,h,:] = q_proj[t,h,:] W_K[:,h,:]^T
+    (ta/interface.py:434-435) for 16-bit operands, forward and backward on
+    the row-GEMM and weight-gradient kernels of ``vafa_absorb_project_fwd`` /
+    ``vafa_absorb_project_bwd``.  Each product is rounded once to the input
+    dtype, as the reference's 16-bit GEMMs and their autograd backward
+    (dq_proj = du W_K per head, dq_raw = dq_proj W_Q^T, dW_Q = q_raw^T dq_proj,
+    dW_K = du^T q_proj per head); the weight gradients are summed over fixed
+    token chunks in order (deterministic)."""
 
     @staticmethod
-    def forward(ctx, q_proj: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
-        d_kv, H, D_H = W_K.shape
-        ctx.save_for_backward(q_proj, W_K)
-        if (q_proj.is_cuda and q_proj.dtype in (torch.bfloat16, torch.float16)
-                and W_K.dtype == q_proj.dtype and d_kv % 8 == 0 and D_H % 16 == 0
-                and D_H <= 128):
-            # matrix-core kernel: per-head products written token-major
-            qp = _aligned(q_proj.contiguous())
-            wk = _aligned(W_K.contiguous())
-            u = torch.empty((q_proj.shape[0], H, d_kv), dtype=q_proj.dtype, device=q_proj.device)
-            _lib.check(_lib.lib().vafa_absorb_project_u(
-                qp.data_ptr(), wk.data_ptr(), u.data_ptr(), q_proj.shape[0], H, d_kv, D_H,
-                _lib.dtype_code(q_proj.dtype), _lib.stream_ptr(q_proj.device)))
-            return u
-        blocks = torch.block_diag(*[W_K[:, h, :].t() for h in range(H)])
-        return (q_proj @ blocks).view(q_proj.shape[0], H, d_kv)
+    def forward(ctx, q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
+        T_q, d_q = q_raw.shape
+        _, H, D_H = W_Q.shape
+        d_kv = W_K.shape[0]
+        L = _lib.lib()
+        q_raw = _aligned(q_raw.contiguous())
+        W_Q = _aligned(W_Q.contiguous())
+        W_K = _aligned(W_K.contiguous())
+        q_proj = torch.empty((T_q, H * D_H), dtype=q_raw.dtype, device=q_raw.device)
+        u = torch.empty((T_q, H, d_kv), dtype=q_raw.dtype, device=q_raw.device)
+        ws = _workspace(L.vafa_absorb_project_workspace(T_q, H, d_q, d_kv, D_H, 0), q_raw.device)
+        _lib.check(L.vafa_absorb_project_fwd(
+            q_raw.data_ptr(), W_Q.data_ptr(), W_K.data_ptr(), q_proj.data_ptr(), u.data_ptr(),
+            T_q, H, d_q, d_kv, D_H, _lib.dtype_code(q_raw.dtype), ws.data_ptr(), ws.numel(),
+            _lib.stream_ptr(q_raw.device)))
+        ctx.save_for_backward(q_raw, W_Q, W_K, q_proj)
+        return u
 
     @staticmethod
     def backward(ctx, du: torch.Tensor):
-        q_proj, W_K = ctx.saved_tensors
+        q_raw, W_Q, W_K, q_proj = ctx.saved_tensors
+        T_q, d_q = q_raw.shape
         d_kv, H, D_H = W_K.shape
-        du2 = du.reshape(du.shape[0], H * d_kv)
-        dq = torch.empty_like(q_proj) if ctx.needs_input_grad[0] else None
-        dW = torch.empty_like(W_K) if ctx.needs_input_grad[1] else None
-        for h in range(H):
-            du_h = du2[:, h * d_kv:(h + 1) * d_kv]
-            if dq is not None:
-                dq[:, h * D_H:(h + 1) * D_H] = du_h @ W_K[:, h, :]
-            if dW is not None:
-                dW[:, h, :] = du_h.t() @ q_proj[:, h * D_H:(h + 1) * D_H]
-        return dq, dW
+        need_q, need_wq, need_wk = ctx.needs_input_grad[:3]
+        du = _aligned(du.contiguous())
+        dq = torch.empty_like(q_raw) if need_q else None
+        dwq = torch.empty_like(W_Q) if need_wq else None
+        dwk = torch.empty_like(W_K) if need_wk else None
+        L = _lib.lib()
+        ws = _workspace(L.vafa_absorb_project_workspace(T_q, H, d_q, d_kv, D_H, 1), du.device)
+
+        def ptr(t):
+            return t.data_ptr() if t is not None else None
+
+        _lib.check(L.vafa_absorb_project_bwd(
+            q_raw.data_ptr(), W_Q.data_ptr(), W_K.data_ptr(), q_proj.data_ptr(), du.data_ptr(),
+            ptr(dq), ptr(dwq), ptr(dwk), T_q, H, d_q, d_kv, D_H, _lib.dtype_code(du.dtype),
+            ws.data_ptr(), ws.numel(), _lib.stream_ptr(du.device)))
+        return dq, dwq, dwk
 
 
 def _project_u(q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
-    """u[t,h,:] = (q_raw[t] W_Q[:,h,:]) W_K[:,h,:]^T (ta/interface.py:434-435).
-
-    One 2-D GEMM for all heads of W_Q (rounded to the input dtype, as the
-    reference's q projection is), then ``_HeadProject`` for W_K: u comes out
+    """u[t,h,:] = (q_raw[t] W_Q[:,h,:]) W_K[:,h,:]^T (ta/interface.py:434-435),
     contiguous ``[T_q, H, d_kv]``.
+
+    16-bit operands with D_Q, D_KV, D_H multiples of 8 run on ``_Project``
+    (both directions in this library's kernels).  Other operands (fp32, odd
+    widths) take the reference's own formulation on torch's GEMMs: q_proj =
+    q_raw @ W_Q, then u = q_proj @ blockdiag(W_K[:,h,:]^T), ONE GEMM that
+    writes u token-major (for finite q_proj the zero blocks add exact zeros
+    to each fp32 sum, so every u element is the same sum of products as per
+    head).
     """
+    if _project_native(q_raw, W_Q, W_K):
+        return _Project.apply(q_raw, W_Q, W_K)
     T_q, d_q = q_raw.shape
     _, H, D_H = W_Q.shape
     q_proj = q_raw @ W_Q.reshape(d_q, H * D_H)
-    return _HeadProject.apply(q_proj, W_K)
+    blocks = torch.block_diag(*[W_K[:, h, :].t() for h in range(H)])
+    return (q_proj @ blocks).view(T_q, H, W_K.shape[0])
 
 
 def packed_target_attn(

@@ -261,71 +261,6 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 }
 
 
-// Head projection of packed_target_attn (ta/interface.py:434-435):
-// u[t, h, f] = sum_d q_proj[t, h*DH + d] W_K[f, h, d], fp32 accumulation and
-// one rounding to T.  One wave per (32 tokens, head): u^T tiles (16 f x 16
-// tokens) = W_K,h (16 f x 32 d) q_proj,h^T (32 d x 16 tokens) on 16x16x32
-// products, every W_K operand feeding both 16-token halves; u is written
-// token-major [T, H, F] directly (four consecutive f per lane).
-constexpr int kProjTok = 32;  // tokens per wave
-
-template <typename T>
-__global__ __launch_bounds__(256) void absorb_project_u_kernel(
-    const T *__restrict__ qp, const T *__restrict__ wk, T *__restrict__ u, int64_t T_q, int H,
-    int F, int DH) {
-  using M16 = Mfma16<T>;
-  using v8 = typename Mfma<T>::v8;
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t ntt = (T_q + kProjTok - 1) / kProjTok;
-  if (wid >= ntt * H) return;
-  const int h = (int)(wid % H);
-  const int64_t tb = (wid / H) * kProjTok;
-  const int l16 = lane & 15, lq = lane >> 4;
-  const int nkc = (DH + 31) / 32;  // <= 4
-  v8 qb[2][4];
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    const int64_t t = tb + hf * 16 + l16;
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      const int d0 = kc * 32 + lq * 8;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (kc < nkc && t < T_q && d0 < DH)
-        w = *reinterpret_cast<const u32x4 *>(qp + (t * H + h) * DH + d0);
-      qb[hf][kc] = as_v8<T>(w);
-    }
-  }
-  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-  for (int ft = 0; ft < (F + 15) / 16; ++ft) {
-    const int f = ft * 16 + l16;
-    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      if (kc >= nkc) break;
-      const int d0 = kc * 32 + lq * 8;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (f < F && d0 < DH)
-        w = *reinterpret_cast<const u32x4 *>(wk + ((int64_t)f * H + h) * DH + d0);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) acc[hf] = M16::mma(as_v8<T>(w), qb[hf][kc], acc[hf]);
-    }
-    // lane: token tb + 16*hf + l16, f = 16*ft + 4*lq + r
-    const int fo = ft * 16 + lq * 4;
-    if (fo < F) {
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int64_t t = tb + hf * 16 + l16;
-        if (t >= T_q) continue;
-        T4 o;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(acc[hf][r]);
-        *reinterpret_cast<T4 *>(u + (t * H + h) * F + fo) = o;
-      }
-    }
-  }
-}
-
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   const int smem = AbsSmem<FP>::kLoopBytes;
@@ -385,25 +320,6 @@ void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
   }
 }
 
-// The head projection kernel takes D_KV a multiple of 8 and D_H a multiple of
-// 16 up to 128.
-bool absorb_project_supported(int F, int DH) {
-  return F > 0 && F % 8 == 0 && DH >= 16 && DH <= 128 && DH % 16 == 0;
-}
-
-template <typename T>
-void launch_absorb_project_u(const void *q_proj, const void *wk, void *u, int64_t T_q, int H,
-                             int F, int DH, hipStream_t st) {
-  const int64_t waves = (T_q + kProjTok - 1) / kProjTok * H;
-  if (waves == 0) return;
-  hipLaunchKernelGGL(absorb_project_u_kernel<T>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
-                     st, (const T *)q_proj, (const T *)wk, (T *)u, T_q, H, F, DH);
-}
-
-template void launch_absorb_project_u<bf16>(const void *, const void *, void *, int64_t, int,
-                                            int, int, hipStream_t);
-template void launch_absorb_project_u<f16>(const void *, const void *, void *, int64_t, int, int,
-                                           int, hipStream_t);
 template bool mfma_absorb_supported<bf16>(int, int, int);
 template bool mfma_absorb_supported<f16>(int, int, int);
 template void launch_mfma_absorb_fwd<bf16>(const AbsorbArgs &, hipStream_t);

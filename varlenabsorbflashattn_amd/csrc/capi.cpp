@@ -2,7 +2,9 @@
 // dispatch.  Compiled by hipcc (host code only; kernels live in *.hip).
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
@@ -307,6 +309,125 @@ int scratch_ptr(void **out) {
   return VAFA_OK;
 }
 
+
+// Projection shapes: every dimension a positive multiple of 8 (16-byte rows
+// for the row GEMM's loads), H * D_H and the token count within int range.
+int check_project_dims(const char *what, int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV,
+                       int64_t D_H) {
+  const bool ok = T_q >= 0 && T_q < (1ll << 31) && H >= 1 && H <= 1024 && D_Q >= 8 &&
+                  D_Q <= 65536 && D_Q % 8 == 0 && D_KV >= 8 && D_KV <= 65536 && D_KV % 8 == 0 &&
+                  D_H >= 8 && D_H % 8 == 0 && H * D_H <= 65536;
+  if (!ok)
+    return fail(VAFA_ERR_VALUE, "%s: T_q=%lld H=%lld D_Q=%lld D_KV=%lld D_H=%lld not supported "
+                "(D_Q, D_KV, D_H positive multiples of 8, H*D_H <= 65536)", what, (long long)T_q,
+                (long long)H, (long long)D_Q, (long long)D_KV, (long long)D_H);
+  return VAFA_OK;
+}
+
+int check_aligned(const char *what, std::initializer_list<const void *> ptrs) {
+  for (const void *p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(VAFA_ERR_VALUE, "%s: operands must be 16-byte aligned", what);
+  return VAFA_OK;
+}
+
+template <typename T>
+void project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q, int H, int F, int DH,
+               hipStream_t st) {
+  // u[t, h, f] = sum_d q_proj[t, h, d] W_K[f, h, d]
+  const int64_t HD = (int64_t)H * DH;
+  launch_rowgemm<T>(RowGemm{q_proj, W_K, u, T_q, H, F, DH, HD, DH, DH, HD, (int64_t)H * F, F}, st);
+}
+
+// Token chunks of a projection weight gradient: on the 16-bit kernel a
+// multiple of 32 tokens, about kWgradWgs workgroups in all (wgs_per_chunk per
+// chunk); on the fp32-product fallback (F > 512) 64 chunks.
+constexpr int64_t kWgradWgs = 512;
+struct Chunks {
+  int64_t tchunk = 0, n = 0;
+};
+Chunks wgrad_chunks(int64_t T_q, int64_t F, int64_t wgs_per_chunk) {
+  Chunks c;
+  if (T_q <= 0) return c;
+  if (!wgrad16_supported((int)F)) {
+    c.tchunk = (T_q + 63) / 64;
+  } else {
+    const int64_t tiles = (T_q + 31) / 32;
+    int64_t want = kWgradWgs / wgs_per_chunk;
+    want = want < 1 ? 1 : (want > tiles ? tiles : want);
+    c.tchunk = (tiles + want - 1) / want * 32;
+  }
+  c.n = (T_q + c.tchunk - 1) / c.tchunk;
+  return c;
+}
+
+struct ProjectWs {
+  void *wt = nullptr;      // W_Q^T [HD, D_Q] (forward) or W_K^T [HD, D_KV] (backward)
+  void *dq_proj = nullptr; // [T_q, HD]
+  float *part = nullptr;   // weight-gradient chunk partials
+  Chunks ck, cq;           // chunks of dW_K and dW_Q
+  int64_t bytes = 0;
+};
+
+ProjectWs carve_project(void *ws, int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV, int64_t D_H,
+                        bool bwd) {
+  Carver c(ws);
+  ProjectWs w;
+  const int64_t HD = H * D_H;
+  w.wt = c.take<void>(HD * (bwd ? D_KV : D_Q) * 2);
+  if (bwd) {
+    w.dq_proj = c.take<void>(T_q * HD * 2);
+    w.ck = wgrad_chunks(T_q, D_KV, H * ((D_H + 31) / 32));
+    w.cq = wgrad_chunks(T_q, D_Q, (HD + 31) / 32);
+    const int64_t pk = w.ck.n * D_KV * HD, pq = w.cq.n * D_Q * HD;
+    w.part = c.take<float>((pk > pq ? pk : pq) * 4 + 4);
+  }
+  w.bytes = c.used;
+  return w;
+}
+
+template <typename T>
+void project_fwd(const void *q_raw, const void *W_Q, const void *W_K, void *q_proj, void *u,
+                 int64_t T_q, int H, int DQ, int F, int DH, const ProjectWs &w, hipStream_t st) {
+  const int HD = H * DH;
+  // q_proj [T, HD] = q_raw [T, DQ] . W_Q [DQ, HD], through W_Q^T [HD, DQ]
+  launch_transpose2d<T>(W_Q, w.wt, DQ, HD, st);
+  launch_rowgemm<T>(RowGemm{q_raw, w.wt, q_proj, T_q, 1, HD, DQ, DQ, 0, 0, DQ, HD, 0}, st);
+  project_u<T>(q_proj, W_K, u, T_q, H, F, DH, st);
+}
+
+template <typename T>
+void project_bwd(const void *q_raw, const void *W_Q, const void *W_K, const void *q_proj,
+                 const void *du, void *dq_raw, void *dW_Q, void *dW_K, int64_t T_q, int H, int DQ,
+                 int F, int DH, const ProjectWs &w, hipStream_t st) {
+  const int HD = H * DH;
+  const bool need_dq = dq_raw != nullptr || dW_Q != nullptr;
+  // W_K^T [HD, F]: the dq_proj product's weight rows
+  if (need_dq) launch_transpose2d<T>(W_K, w.wt, F, HD, st);
+  // dW_K[f, h, d] = sum_t du[t, h, f] q_proj[t, h, d], and on the 16-bit
+  // kernel dq_proj[t, h, d] = sum_f du[t, h, f] W_K[f, h, d] from the same du reads
+  const bool fused = wgrad16_supported(F) && dW_K != nullptr;
+  if (fused) {
+    launch_wgrad16<T>(Wgrad{du, q_proj, w.wt, need_dq ? w.dq_proj : nullptr, dW_K, w.part, T_q,
+                            w.ck.tchunk, w.ck.n, H, F, DH}, st);
+  } else if (dW_K != nullptr) {
+    launch_wgrad<T, T>(du, q_proj, w.part, dW_K, T_q, w.ck.tchunk, w.ck.n, H, F, DH, st);
+  }
+  if (!need_dq) return;
+  if (!fused)
+    launch_rowgemm<T>(RowGemm{du, w.wt, w.dq_proj, T_q, H, DH, F, (int64_t)H * F, F,
+                              (int64_t)DH * F, F, HD, DH}, st);
+  if (dq_raw != nullptr)  // dq_raw [T, DQ] = dq_proj [T, HD] . W_Q [DQ, HD]^T
+    launch_rowgemm<T>(RowGemm{w.dq_proj, W_Q, dq_raw, T_q, 1, DQ, HD, HD, 0, 0, HD, DQ, 0}, st);
+  if (dW_Q != nullptr) {  // dW_Q[c, hd] = sum_t q_raw[t, c] dq_proj[t, hd]
+    if (wgrad16_supported(DQ))
+      launch_wgrad16<T>(Wgrad{q_raw, w.dq_proj, nullptr, nullptr, dW_Q, w.part, T_q, w.cq.tchunk,
+                              w.cq.n, 1, DQ, HD}, st);
+    else
+      launch_wgrad<T, T>(q_raw, w.dq_proj, w.part, dW_Q, T_q, w.cq.tchunk, w.cq.n, 1, DQ, HD, st);
+  }
+}
+
 }  // namespace
 }  // namespace vafa
 
@@ -468,24 +589,78 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
 
 int vafa_absorb_project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q, int64_t H,
                           int64_t D_KV, int64_t D_H, int32_t dtype, void *stream) {
-  if (T_q < 0 || H < 1 || H > 1024)
-    return fail(VAFA_ERR_VALUE, "project_u: bad T_q=%lld / H=%lld", (long long)T_q, (long long)H);
-  if (!absorb_project_supported((int)D_KV, (int)D_H))
-    return fail(VAFA_ERR_VALUE, "project_u: D_KV=%lld (multiple of 8) / D_H=%lld "
-                "(multiple of 16, <= 128) not supported", (long long)D_KV, (long long)D_H);
+  if (int rc = check_project_dims("project_u", T_q, H, 8, D_KV, D_H)) return rc;
+  if (int rc = check_aligned("project_u", {q_proj, W_K, u})) return rc;
   switch (dtype) {
     case VAFA_BF16:
-      launch_absorb_project_u<bf16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H,
-                                    (hipStream_t)stream);
+      project_u<bf16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H, (hipStream_t)stream);
       break;
     case VAFA_F16:
-      launch_absorb_project_u<f16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H,
-                                   (hipStream_t)stream);
+      project_u<f16>(q_proj, W_K, u, T_q, (int)H, (int)D_KV, (int)D_H, (hipStream_t)stream);
       break;
     default:
       return fail(VAFA_ERR_VALUE, "project_u: 16-bit dtypes only (got %d)", (int)dtype);
   }
   return check_launch("vafa_absorb_project_u");
+}
+
+int64_t vafa_absorb_project_workspace(int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV,
+                                      int64_t D_H, int32_t backward) {
+  if (check_project_dims("project_workspace", T_q, H, D_Q, D_KV, D_H) != VAFA_OK) return -1;
+  return carve_project(nullptr, T_q, H, D_Q, D_KV, D_H, backward != 0).bytes;
+}
+
+int vafa_absorb_project_fwd(const void *q_raw, const void *W_Q, const void *W_K, void *q_proj,
+                            void *u, int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV,
+                            int64_t D_H, int32_t dtype, void *workspace, int64_t workspace_bytes,
+                            void *stream) {
+  if (int rc = check_project_dims("project_fwd", T_q, H, D_Q, D_KV, D_H)) return rc;
+  if (int rc = check_aligned("project_fwd", {q_raw, W_Q, W_K, q_proj, u, workspace})) return rc;
+  const ProjectWs w = carve_project(workspace, T_q, H, D_Q, D_KV, D_H, false);
+  if (workspace_bytes < w.bytes || workspace == nullptr)
+    return fail(VAFA_ERR_WORKSPACE, "project_fwd: workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case VAFA_BF16:
+      project_fwd<bf16>(q_raw, W_Q, W_K, q_proj, u, T_q, (int)H, (int)D_Q, (int)D_KV, (int)D_H, w, st);
+      break;
+    case VAFA_F16:
+      project_fwd<f16>(q_raw, W_Q, W_K, q_proj, u, T_q, (int)H, (int)D_Q, (int)D_KV, (int)D_H, w, st);
+      break;
+    default:
+      return fail(VAFA_ERR_VALUE, "project_fwd: 16-bit dtypes only (got %d)", (int)dtype);
+  }
+  return check_launch("vafa_absorb_project_fwd");
+}
+
+int vafa_absorb_project_bwd(const void *q_raw, const void *W_Q, const void *W_K,
+                            const void *q_proj, const void *du, void *dq_raw, void *dW_Q,
+                            void *dW_K, int64_t T_q, int64_t H, int64_t D_Q, int64_t D_KV,
+                            int64_t D_H, int32_t dtype, void *workspace, int64_t workspace_bytes,
+                            void *stream) {
+  if (int rc = check_project_dims("project_bwd", T_q, H, D_Q, D_KV, D_H)) return rc;
+  if (int rc = check_aligned("project_bwd", {q_raw, W_Q, W_K, q_proj, du, dq_raw, dW_Q, dW_K,
+                                             workspace}))
+    return rc;
+  const ProjectWs w = carve_project(workspace, T_q, H, D_Q, D_KV, D_H, true);
+  if (workspace_bytes < w.bytes || workspace == nullptr)
+    return fail(VAFA_ERR_WORKSPACE, "project_bwd: workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case VAFA_BF16:
+      project_bwd<bf16>(q_raw, W_Q, W_K, q_proj, du, dq_raw, dW_Q, dW_K, T_q, (int)H, (int)D_Q,
+                        (int)D_KV, (int)D_H, w, st);
+      break;
+    case VAFA_F16:
+      project_bwd<f16>(q_raw, W_Q, W_K, q_proj, du, dq_raw, dW_Q, dW_K, T_q, (int)H, (int)D_Q,
+                       (int)D_KV, (int)D_H, w, st);
+      break;
+    default:
+      return fail(VAFA_ERR_VALUE, "project_bwd: 16-bit dtypes only (got %d)", (int)dtype);
+  }
+  return check_launch("vafa_absorb_project_bwd");
 }
 
 int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O,

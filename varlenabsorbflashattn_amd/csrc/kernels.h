@@ -79,6 +79,16 @@ void launch_sum_combine(const float *part, void *out, const int32_t *comb_items,
 // dW_V = sum_t aX[t]^T dO[t] per head, two-level deterministic reduction.
 template <typename T>
 void launch_absorb_dwv(const AbsorbArgs &, hipStream_t);
+// Weight gradient out[f, g, d] = sum_t A[t, g, f] B[t, g, d] (A [T, G, F], B
+// [T, G, DH], out in B's dtype): ordered fp32 partials over n_chunks token
+// chunks of tchunk tokens (part holds n_chunks * F * G * DH floats), then
+// their sum in chunk order.  TA is float or T.
+template <typename TA, typename T>
+void launch_wgrad(const void *a, const void *b, float *part, void *out, int64_t T_q,
+                  int64_t tchunk, int64_t n_chunks, int G, int F, int DH, hipStream_t);
+// out[o] = sum_c part[c * n_out + o] in chunk order, rounded to T
+template <typename T>
+void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chunks, hipStream_t);
 // dAX = dO W_V^T, fp32 [T_q, H, F]
 template <typename T>
 void launch_absorb_dax(const AbsorbArgs &, hipStream_t);
@@ -94,10 +104,36 @@ template <typename T, int D> void launch_mfma_varlen_fkv(const VarlenArgs &, hip
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
-bool absorb_project_supported(int F, int DH);
-template <typename T>
-void launch_absorb_project_u(const void *q_proj, const void *wk, void *u, int64_t T_q, int H,
-                             int F, int DH, hipStream_t st);
+
+// absorb_project.hip (bf16 / f16): Y[t, g*ys + j] = sum_k X[t*ldx + g*xs + k]
+// * W[g*ws + j*ldw + k] for t < T_q, g < G, j < J, k < K; fp32 accumulation,
+// one rounding.  Needs K % 8 == 0, J % 8 == 0, every stride % 8 == 0 and
+// 16-byte aligned X, W, Y.
+struct RowGemm {
+  const void *X, *W;
+  void *Y;
+  int64_t T_q;
+  int G, J, K;
+  int64_t ldx, xs, ws, ldw, ldy, ys;
+};
+bool rowgemm_supported(const RowGemm &);
+// Weight gradient out[f, g, d] = sum_t A[t, g, f] B[t, g, d] on 16-bit
+// matrix cores (A [T, G, F] with F <= 512, B [T, G, DH]): fp32 partials over
+// n_chunks chunks of tchunk tokens (a multiple of 32; part holds n_chunks * F
+// * G * DH floats) summed in chunk order into out.  With dq != nullptr also
+// dq[t, g, d] = sum_f A[t, g, f] Wt[g, d, f] (Wt [G, DH, F]), rounded once.
+struct Wgrad {
+  const void *A, *B, *Wt;
+  void *dq, *out;
+  float *part;
+  int64_t T_q, tchunk, n_chunks;
+  int G, F, DH;
+};
+bool wgrad16_supported(int F);
+template <typename T> void launch_wgrad16(const Wgrad &, hipStream_t);
+template <typename T> void launch_rowgemm(const RowGemm &, hipStream_t);
+// dst [C, R] = src [R, C]^T
+template <typename T> void launch_transpose2d(const void *src, void *dst, int R, int C, hipStream_t);
 // absorb_bwd_mfma.hip: du/aX (query side) and dX (key side) on matrix cores
 template <typename T> void launch_mfma_absorb_du(const AbsorbArgs &, hipStream_t);
 // dAX = dO W_V^T; false (nothing launched) for a D_H it does not cover

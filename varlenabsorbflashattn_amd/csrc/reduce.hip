@@ -202,11 +202,13 @@ __global__ __launch_bounds__(256) void absorb_dax_kernel(const T *__restrict__ d
   }
 }
 
-// dW_V partial over one token chunk, part[c, f, h, d] = sum_{t in chunk}
-// aX[t,h,f] dO[t,h,d], on fp32 matrix cores (v_mfma_f32_32x32x2f32, aX kept in
-// fp32).  One wave per (chunk, head, 32-wide f slice, 32-wide d tile):
-// dW_V^T[d, f] += dO^T[d, t] aX[t, f] two tokens per product, lane l feeding
-// token t + l/32 at d (A) and f (B) = l % 32.
+// Weight-gradient partial over one token chunk, part[c, f, h, d] =
+// sum_{t in chunk} A[t,h,f] B[t,h,d] (dW_V: A = aX in fp32, B = dO; the
+// projections' dW_K: A = du, B = q_proj; dW_Q: one group, A = q_raw, B =
+// dq_proj), on fp32 matrix cores (v_mfma_f32_32x32x2f32).  One wave per
+// (chunk, head, 32-wide f slice, 32-wide d tile): part^T[d, f] += B^T[d, t]
+// A[t, f] two tokens per product, lane l feeding token t + l/32 at d (A
+// operand) and f (B operand) = l % 32.
 template <typename T>
 __device__ __forceinline__ float bits_to_f(uint32_t b) {
   if constexpr (std::is_same<T, float>::value) return __uint_as_float(b);
@@ -214,9 +216,9 @@ __device__ __forceinline__ float bits_to_f(uint32_t b) {
   else return (float)__builtin_bit_cast(f16, (uint16_t)b);
 }
 
-template <typename T>
+template <typename TA, typename T>
 __global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
-    const float *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
+    const TA *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
     int64_t T_q, int64_t tchunk, int H, int F, int DH, int n_waves) {
   const int lane = threadIdx.x, l32 = lane & 31, kt = lane >> 5;
   const int nfs = (F + 31) / 32, nds = (DH + 31) / 32;
@@ -243,21 +245,22 @@ __global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
   // trip (predicated loads compile to branches that wait on each load).
   const int dc = d_ok ? d : DH - 1, fc = f_ok ? f : F - 1;
   auto load = [&](int64_t t, float(&av)[kU], float(&bv)[kU]) {
-    // dO bits go into separate 32-bit registers: 16-bit elements loaded as T
+    // 16-bit elements go into separate 32-bit registers: loaded as T they
     // get packed two per register, and each load then waits on the previous
     using Bits = typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type;
-    uint32_t ra[kU];
+    using BitsA = typename std::conditional<sizeof(TA) == 2, uint16_t, uint32_t>::type;
+    uint32_t ra[kU], rb[kU];
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
       const int64_t tt = t + 2 * i + kt, tc = tt < tb ? tt : tb - 1;
       ra[i] = reinterpret_cast<const Bits *>(dO)[(tc * H + h) * DH + dc];
-      bv[i] = ax[(tc * H + h) * F + fc];
+      rb[i] = reinterpret_cast<const BitsA *>(ax)[(tc * H + h) * F + fc];
     }
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
       const bool ok = t + 2 * i + kt < tb;
       av[i] = ok && d_ok ? bits_to_f<T>(ra[i]) : 0.f;
-      bv[i] = ok && f_ok ? bv[i] : 0.f;
+      bv[i] = ok && f_ok ? bits_to_f<TA>(rb[i]) : 0.f;
     }
   };
   auto product = [&](const float(&av)[kU], const float(&bv)[kU]) {
@@ -353,17 +356,32 @@ void launch_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
                      (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.H, a.F, a.DH);
 }
 
+template <typename TA, typename T>
+void launch_wgrad(const void *a, const void *b, float *part, void *out, int64_t T_q,
+                  int64_t tchunk, int64_t n_chunks, int G, int F, int DH, hipStream_t st) {
+  const int64_t n_out = (int64_t)F * G * DH;
+  if (n_chunks > 0) {
+    const int64_t waves = n_chunks * G * ((F + 31) / 32) * ((DH + 31) / 32);
+    const int64_t grid = (waves + kXcds - 1) / kXcds * kXcds;
+    hipLaunchKernelGGL((absorb_dwv_part_kernel<TA, T>), dim3((unsigned)grid), dim3(64), 0, st,
+                       (const TA *)a, (const T *)b, part, T_q, tchunk, G, F, DH, (int)waves);
+  }
+  hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st, part,
+                     (T *)out, n_out, n_chunks);
+}
+
+template <typename T>
+void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chunks,
+                      hipStream_t st) {
+  if (n_out == 0) return;
+  hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st, part,
+                     (T *)out, n_out, n_chunks);
+}
+
 template <typename T>
 void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
-  const int64_t n_out = (int64_t)a.F * a.H * a.DH;
-  if (a.n_tchunks > 0) {
-    const int64_t waves = a.n_tchunks * a.H * ((a.F + 31) / 32) * ((a.DH + 31) / 32);
-    const int64_t grid = (waves + kXcds - 1) / kXcds * kXcds;
-    hipLaunchKernelGGL(absorb_dwv_part_kernel<T>, dim3((unsigned)grid), dim3(64), 0, st, a.ax,
-                       (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH, (int)waves);
-  }
-  hipLaunchKernelGGL(absorb_dwv_sum_kernel<T>, dim3(blocks_for(n_out)), dim3(256), 0, st,
-                     a.dwv_part, (T *)a.dwv, n_out, a.n_tchunks);
+  launch_wgrad<float, T>(a.ax, a.dO, a.dwv_part, a.dwv, a.T_q, a.tchunk, a.n_tchunks, a.H, a.F,
+                         a.DH, st);
 }
 
 #define VAFA_INST(T)                                                                        \
@@ -374,7 +392,10 @@ void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
   template void launch_sum_combine<T>(const float *, void *, const int32_t *, int64_t, int, \
                                       int, int, hipStream_t);                               \
   template void launch_absorb_dax<T>(const AbsorbArgs &, hipStream_t);                      \
-  template void launch_absorb_dwv<T>(const AbsorbArgs &, hipStream_t);
+  template void launch_absorb_dwv<T>(const AbsorbArgs &, hipStream_t);                      \
+  template void launch_wgrad<T, T>(const void *, const void *, float *, void *, int64_t,    \
+                                   int64_t, int64_t, int, int, int, hipStream_t);           \
+  template void launch_chunk_sum<T>(const float *, void *, int64_t, int64_t, hipStream_t);
 VAFA_INST(float)
 VAFA_INST(f16)
 VAFA_INST(bf16)

@@ -297,6 +297,36 @@ def bench_absorb_bwd(case, iters, d_q=None, dtype=None):
     return st, f_st
 
 
+def bench_absorb_full(case, iters):
+    """The whole packed_target_attn (projections included) through the
+    prepared-index contract: returns (fwd+bwd, fwd) stats."""
+    import torch
+    from varlenabsorbflashattn_amd import packed_target_attn
+    q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case)
+    ins = [t.detach().clone().requires_grad_(True) for t in (q_raw, X, W_Q, W_K, W_V)]
+    g = torch.Generator().manual_seed(1)
+    dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(u.device, u.dtype)
+
+    def call():
+        return packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck, q_chunk_indices=qi,
+                                  k_chunk_indices=ki, validate=False)
+
+    def step():
+        call().backward(dO)
+        for t in ins:
+            t.grad = None
+
+    def fwd():
+        with torch.no_grad():
+            call()
+
+    st = timed(step, iters)
+    f_st = timed(fwd, iters)
+    del ins, q_raw, X, u, dO
+    torch.cuda.empty_cache()
+    return st, f_st
+
+
 def absorb_line(case, st, full_st=None):
     gbs = case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9
     out = {"ms": st, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
@@ -447,29 +477,8 @@ def run_only(which, steps, warmup):
     if which == "replay":
         return bench_replay(max(steps, 1), warmup)
     if which == "c4full":
-        # the whole packed_target_attn (u projection included), fwd and fwd+bwd
-        from varlenabsorbflashattn_amd import packed_target_attn
         case = W.config4(seed=0)
-        q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case)
-        ins = [t.detach().clone().requires_grad_(True) for t in (q_raw, X, W_Q, W_K, W_V)]
-        g = torch.Generator().manual_seed(1)
-        dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(u.device, u.dtype)
-
-        def call():
-            return packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck, q_chunk_indices=qi,
-                                      k_chunk_indices=ki, validate=False)
-
-        def step():
-            call().backward(dO)
-            for t in ins:
-                t.grad = None
-
-        def fwd():
-            with torch.no_grad():
-                call()
-
-        st = timed(step, max(steps, 1))
-        f_st = timed(fwd, max(steps, 1))
+        st, f_st = bench_absorb_full(case, max(steps, 1))
         return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st}
     if which in ("c4b", "c4_fp32"):
         case = W.config4(seed=0)
@@ -532,9 +541,11 @@ def main():
             log(cfg.name, st["mean"], secondary[cfg.name + "_fwd"]["GB/s"])
         c4 = W.config4(seed=0)
         b_st, bf_st = bench_absorb_bwd(c4, n2)
+        p_st, _ = bench_absorb_full(c4, n2)
         secondary[c4.name + "_fwd_bwd"] = {"ms": b_st, "fwd_ms": bf_st,
-                                           "bwd_ms": b_st["mean"] - bf_st["mean"]}
-        log(c4.name + " fwd+bwd", b_st["mean"], bf_st["mean"])
+                                           "bwd_ms": b_st["mean"] - bf_st["mean"],
+                                           "packed_target_attn_fwd_bwd_ms": p_st}
+        log(c4.name + " fwd+bwd", b_st["mean"], bf_st["mean"], "full op", p_st["mean"])
         # the reference's documented absorb call is fp32 (no bf16 flag)
         b_st, bf_st = bench_absorb_bwd(c4, n2, dtype=torch.float32)
         c4f = W.AbsorbCase(c4.name, c4.q_lens, c4.k_lens, c4.H, c4.D_H, c4.D_in, torch.float32)

@@ -70,6 +70,11 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
   const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
 }
+// The same for a wave-uniform byte count below 2^31 (no 64-bit clamp).
+__device__ __forceinline__ rsrc_t make_rsrc32(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int32_t)bytes,
+                                           0x00020000);
+}
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
@@ -91,6 +96,28 @@ __device__ __forceinline__ u32x4 rsrc_words(const void *base, int64_t bytes) {
   r[2] = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : bytes));
   r[3] = 0x00020000u;
   return r;
+}
+
+// The same for a wave-uniform byte count below 2^31, formed on the scalar
+// unit (no 64-bit clamp: SALU has no signed 64-bit compare, so the clamp of
+// rsrc_words runs on the vector unit).
+__device__ __forceinline__ u32x4 rsrc_words32(const void *base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 r;
+  r[0] = (uint32_t)a;
+  r[1] = (uint32_t)(a >> 32) & 0xffffu;
+  r[2] = bytes;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// min(max(n, 0), hi), made wave-uniform: a clamp compiles to v_med3_i32,
+// which would drag the byte counts formed from it (and their 64-bit
+// multiplies) onto the vector unit.
+__device__ __forceinline__ int uniform_clamp(int n, int hi) {
+  n = n < hi ? n : hi;
+  n = n > 0 ? n : 0;
+  return __builtin_amdgcn_readfirstlane(n);
 }
 
 __device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t lds_base, int32_t voff) {

@@ -21,6 +21,8 @@
 // per lane (lane <-> query row); the dK/dV kernel reads LSE and delta of its
 // 32-row block from LDS.  LDS operands are read a few products ahead of the
 // MFMAs that consume them (sched_barrier keeps that order).
+#include <type_traits>
+
 #include "kernels.h"
 #include "mfma.h"
 
@@ -65,8 +67,8 @@ template <typename T, int D>
 __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
                                          uint32_t base, int wave, int lane) {
   constexpr int RS = D + kPad;
-  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
-  const u32x4 rs = rsrc_words(src + (int64_t)r0 * H * D, (int64_t)(rows > 0 ? rows : 0) * H * D * 2);
+  const int rows = uniform_clamp(r_end - r0, kRB);
+  const u32x4 rs = rsrc_words32(src + (int64_t)r0 * H * D, (uint32_t)(rows * H * D * 2));
   const int off = (wave * 8 * H + h) * D * 2 + lane * 16;
   if (lane < D / 8) {
 #pragma unroll
@@ -110,8 +112,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     dma_rows<T, D>(q, qb, q1, H, h, lds_addr(base), wave, lane);
     dma_rows<T, D>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
     const float *vec = (wave & 1) ? delta : lse;
-    const int rows = q1 - qb < kRB ? q1 - qb : kRB;
-    const u32x4 rv = rsrc_words(vec + (int64_t)qb * H + h, (int64_t)(rows > 0 ? rows : 0) * H * 4);
+    const int rows = uniform_clamp(q1 - qb, kRB);
+    const u32x4 rv = rsrc_words32(vec + (int64_t)qb * H + h, (uint32_t)(rows * H * 4));
     if (lane < kRB) lds_dma4(rv, lds_addr(base + 2 * S::kQs * 2 + (wave & 1) * kRB * 4), lane * H * 4);
   };
   const int nblk = (q1 - q0 + kRB - 1) / kRB;
@@ -364,8 +366,8 @@ template <typename T, int D, int NT>
 __device__ __forceinline__ void load_rows(Rows<D, NT> &s, const T *__restrict__ src, int r0,
                                           int r_end, int H, int h, int t) {
   constexpr int CPR = D / 8;
-  const int rows = r_end - r0 < kRB ? r_end - r0 : kRB;
-  const rsrc_t rs = make_rsrc(src + (int64_t)r0 * H * D, (int64_t)rows * H * D * 2);
+  const int rows = uniform_clamp(r_end - r0, kRB);
+  const rsrc_t rs = make_rsrc32(src + (int64_t)r0 * H * D, (uint32_t)(rows * H * D * 2));
 #pragma unroll
   for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
     const int ci = t + NT * i;
@@ -491,7 +493,11 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
                     4 * (lane & 3);
   if (nblk > 0) put(0);
   __syncthreads();
-  for (int j = 0; j < nblk; ++j) {
+  // Only the last key block can reach past k1, and only there are the dS
+  // columns of those keys masked: the loop body is instantiated twice so the
+  // other blocks carry no per-element key compares (if-converted, they were
+  // 48 VALU instructions per block).
+  auto block = [&](int j, auto masked) {
     const int kb = k0 + j * kRB;
     if (j + 1 < nblk) load_rows<T, D, 128>(stg, src, kb + kRB, k1, H, h, st);
     if (wave_active) {
@@ -530,10 +536,12 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
         const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lr));
         dp[r] = p * (dp[r] - Dr);
       }
-      if (kb + kRB > k1) {
+      if constexpr (decltype(masked)::value) {
+        if (kb + kRB > k1) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) dp[r] = 0.f;
+          for (int r = 0; r < 16; ++r)
+            if (kb + (r >> 2) * 8 + lhalf * 4 + (r & 3) >= k1) dp[r] = 0.f;
+        }
       }
       typename M::v8 sb[2];
 #pragma unroll
@@ -548,7 +556,10 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     }
     if (j + 1 < nblk) put((j + 1) & 1);
     __syncthreads();
-  }
+  };
+  int j = 0;
+  for (; j + 1 < nblk; ++j) block(j, std::false_type{});
+  if (j < nblk) block(j, std::true_type{});
 
   if (!row_ok) return;
   if (pbase < 0) {

@@ -290,6 +290,130 @@ __global__ __launch_bounds__(64) void absorb_dwv_part_kernel(
   }
 }
 
+// dW_V partials with the chunk's token tiles staged in LDS, one workgroup per
+// (token chunk c, head h, 32-column block of d): part[c, f, h, d] = sum_t
+// aX[t,h,f] dO[t,h,d] on v_mfma_f32_16x16x4f32 (aX stays fp32).  32-token
+// tiles of aX [32][FP] and dO [32][32] (converted to fp32) sit in a double-
+// buffered LDS ring, the next tile's 16-byte loads held in registers while the
+// current one is consumed; every operand is one 4-byte LDS read (A: aX[t =
+// 4*ks + l/16][f = 16*ft + l%16], B: dO[t][d = 16*dt + l%16], rows padded so
+// the four token rows of a read fall in different banks).  Each wave owns f
+// tiles wave + 4j and both d tiles.
+constexpr int kDwTok = 32;
+constexpr int kDwBS = 48;  // B tile row stride (floats)
+
+template <int FP>
+struct DwSmem {
+  static constexpr int AS = FP + 16;  // A tile row stride (floats)
+  static constexpr int kStage = kDwTok * (AS + kDwBS);
+  static constexpr int kBytes = 2 * kStage * 4;
+};
+
+template <typename T, int FP>
+__global__ __launch_bounds__(256) void absorb_dwv_lds_kernel(
+    const float *__restrict__ ax, const T *__restrict__ dO, float *__restrict__ part,
+    int64_t T_q, int64_t tchunk, int H, int F, int DH, int n_db) {
+  static_assert(sizeof(T) == 2, "16-bit dO");
+  using S = DwSmem<FP>;
+  extern __shared__ __align__(16) float dw_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lq = lane >> 4;
+  const int wave = tid >> 6;
+  int64_t b = blockIdx.x;
+  const int db = (int)(b % n_db);
+  b /= n_db;
+  const int h = (int)(b % H);
+  const int64_t c = b / H;
+  const int64_t ta = c * tchunk, tb = ta + tchunk < T_q ? ta + tchunk : T_q;
+  const int d0 = db * 32;
+  const int dn = DH - d0 < 32 ? DH - d0 : 32;
+
+  constexpr int kACh = FP / 4;                 // 16-byte chunks per aX row
+  constexpr int kAPer = kDwTok * kACh / 256;   // per thread
+  u32x4 ra[kAPer], rb = {0u, 0u, 0u, 0u};
+  // branch-free loads: clamped in-range addresses, zeros selected afterwards
+  auto load = [&](int64_t t0) {
+#pragma unroll
+    for (int i = 0; i < kAPer; ++i) {
+      const int idx = i * 256 + tid, r = idx / kACh, ch = idx % kACh;
+      const int64_t t = t0 + r;
+      const bool ok = t < tb && ch * 4 < F;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(ax + (ok ? (t * H + h) * F + ch * 4 : 0));
+      ra[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    const int r = (tid >> 2) & (kDwTok - 1), ch = tid & 3;
+    const int64_t t = t0 + r;
+    const bool ok = tid < kDwTok * 4 && t < tb && ch * 8 < dn;
+    const u32x4 v =
+        *reinterpret_cast<const u32x4 *>(dO + (ok ? (t * H + h) * DH + d0 + ch * 8 : 0));
+    rb = ok ? v : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto stage = [&](int st) {
+    float *as = dw_smem + st * S::kStage;
+    float *bs = as + kDwTok * S::AS;
+#pragma unroll
+    for (int i = 0; i < kAPer; ++i) {
+      const int idx = i * 256 + tid, r = idx / kACh, ch = idx % kACh;
+      *reinterpret_cast<u32x4 *>(as + r * S::AS + ch * 4) = ra[i];
+    }
+    if (tid < kDwTok * 4) {
+      const int r = tid >> 2, ch = tid & 3;
+      f32x4 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = bits_to_f<T>((rb[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+        hi[e] = bits_to_f<T>((rb[(e + 4) >> 1] >> ((e & 1) * 16)) & 0xffffu);
+      }
+      *reinterpret_cast<f32x4 *>(bs + r * kDwBS + ch * 8) = lo;
+      *reinterpret_cast<f32x4 *>(bs + r * kDwBS + ch * 8 + 4) = hi;
+    }
+  };
+
+  constexpr int kFt = FP / 64;  // f tiles per wave
+  f32x4 acc[kFt][2];
+#pragma unroll
+  for (int j = 0; j < kFt; ++j)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) acc[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nt = (int)((tb - ta + kDwTok - 1) / kDwTok);
+  load(ta);
+  stage(0);
+  __syncthreads();
+#pragma nounroll
+  for (int i = 0; i < nt; ++i) {
+    if (i + 1 < nt) load(ta + (int64_t)(i + 1) * kDwTok);
+    const float *as = dw_smem + (i & 1) * S::kStage + lq * S::AS + wave * 16 + l16;
+    const float *bs = dw_smem + (i & 1) * S::kStage + kDwTok * S::AS + lq * kDwBS + l16;
+#pragma unroll
+    for (int ks = 0; ks < kDwTok / 4; ++ks) {
+      float bv[2], av[kFt];
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) bv[dt] = bs[ks * 4 * kDwBS + 16 * dt];
+#pragma unroll
+      for (int j = 0; j < kFt; ++j) av[j] = as[ks * 4 * S::AS + 64 * j];
+#pragma unroll
+      for (int j = 0; j < kFt; ++j)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+          acc[j][dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[dt], acc[j][dt], 0, 0, 0);
+    }
+    if (i + 1 < nt) stage((i + 1) & 1);
+    __syncthreads();
+  }
+  // C[f][d]: f = 16*(wave + 4j) + 4*lq + r, d = d0 + 16*dt + l16
+#pragma unroll
+  for (int j = 0; j < kFt; ++j)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d = 16 * dt + l16;
+      if (d >= dn) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int f = 16 * (wave + 4 * j) + 4 * lq + r;
+        if (f < F) part[((c * F + f) * H + h) * DH + d0 + d] = acc[j][dt][r];
+      }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void absorb_dwv_sum_kernel(const float *__restrict__ part,
                                                              T *__restrict__ dwv, int64_t n_out,
@@ -378,8 +502,32 @@ void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chu
                      (T *)out, n_out, n_chunks);
 }
 
+template <typename T, int FP>
+void dwv_lds(const AbsorbArgs &a, hipStream_t st) {
+  const int n_db = (a.DH + 31) / 32;
+  const int64_t wgs = a.n_tchunks * a.H * n_db;
+  if (wgs > 0) {
+    constexpr int smem = DwSmem<FP>::kBytes;
+    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dwv_lds_kernel<T, FP>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    hipLaunchKernelGGL((absorb_dwv_lds_kernel<T, FP>), dim3((unsigned)wgs), dim3(256), smem, st,
+                       a.ax, (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH, n_db);
+  }
+  launch_chunk_sum<T>(a.dwv_part, a.dwv, (int64_t)a.F * a.H * a.DH, a.n_tchunks, st);
+}
+
+// dW_V: the LDS-tiled kernel for 16-bit dO and D_KV <= 256 (a multiple of
+// 4), the register-batched one otherwise.
 template <typename T>
 void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.F % 4 == 0 && a.F <= 256) {
+      if (a.F <= 64) dwv_lds<T, 64>(a, st);
+      else if (a.F <= 128) dwv_lds<T, 128>(a, st);
+      else dwv_lds<T, 256>(a, st);
+      return;
+    }
+  }
   launch_wgrad<float, T>(a.ax, a.dO, a.dwv_part, a.dwv, a.T_q, a.tchunk, a.n_tchunks, a.H, a.F,
                          a.DH, st);
 }

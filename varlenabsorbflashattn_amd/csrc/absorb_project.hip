@@ -129,6 +129,124 @@ __global__ __launch_bounds__(256) void rowgemm_nt_kernel(
   }
 }
 
+// K <= 256: one workgroup walks tiles_per_wg consecutive 32-token tiles of
+// one (group, column block) with its W operands loaded once into registers;
+// X tiles go through a double-buffered LDS ring (the next tile's 16-byte
+// loads held in registers under the current tile's products), and each
+// tile's Y block is staged in LDS and stored while the next X tile lands.
+template <typename T, int NJ, int KS>
+__global__ __launch_bounds__(256) void rowgemm_tiles_kernel(
+    const T *__restrict__ X, const T *__restrict__ W, T *__restrict__ Y, int64_t T_q, int G,
+    int J, int K, int64_t ldx, int64_t xs, int64_t ws, int64_t ldw, int64_t ldy, int64_t ys,
+    int n_jb, int tiles_per_wg, int64_t n_tt) {
+  using M16 = Mfma16<T>;
+  constexpr int kKBlk = 32 * KS;
+  constexpr int kXS = kKBlk + 16;
+  constexpr int kJB = 64 * NJ;
+  constexpr int kYS = kJB + 8;
+  constexpr int kXElems = kRgTok * kXS;
+  __shared__ __align__(16) T smem[2 * kXElems + kRgTok * kYS];
+  T *ystage = smem + 2 * kXElems;
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lq = lane >> 4;
+  const int wave = tid >> 6;
+  int64_t b = blockIdx.x;
+  const int jb = (int)(b % n_jb);
+  b /= n_jb;
+  const int g = (int)(b % G);
+  const int64_t tt0 = (b / G) * tiles_per_wg;
+  const int64_t tt1 = tt0 + tiles_per_wg < n_tt ? tt0 + tiles_per_wg : n_tt;
+  const T *xg = X + g * xs;
+  const T *wg = W + g * ws;
+
+  // this wave's W operands, loaded once (branch-free: clamped, then zeroed)
+  u32x4 wa[NJ][KS];
+#pragma unroll
+  for (int n = 0; n < NJ; ++n) {
+    const int j = jb * kJB + wave * 16 * NJ + n * 16 + l16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 32 + lq * 8;
+      const bool ok = k < K && j < J;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(wg + (ok ? (int64_t)j * ldw + k : 0));
+      wa[n][ks] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  constexpr int kCh = kKBlk / 8;                          // 16-byte chunks per X row
+  constexpr int kXPer = (kRgTok * kCh + 255) / 256;       // per thread
+  u32x4 rx[kXPer];
+  auto load_x = [&](int64_t tt) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int idx = i * 256 + tid, r = (idx / kCh) & (kRgTok - 1), c = idx % kCh;
+      const int64_t t = tt * kRgTok + r;
+      const bool ok = idx < kRgTok * kCh && t < T_q && c * 8 < K;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(xg + (ok ? t * ldx + c * 8 : 0));
+      rx[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int idx = i * 256 + tid;
+      if (idx < kRgTok * kCh)
+        *reinterpret_cast<u32x4 *>(smem + buf * kXElems + (idx / kCh) * kXS + (idx % kCh) * 8) =
+            rx[i];
+    }
+  };
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
+  constexpr int kYCh = kJB / 8;
+  const int jn = J - jb * kJB < kJB ? J - jb * kJB : kJB;
+  if (tt0 < tt1) {
+    load_x(tt0);
+    store_x(0);
+  }
+  __syncthreads();
+  for (int64_t tt = tt0; tt < tt1; ++tt) {
+    const int buf = (int)((tt - tt0) & 1);
+    if (tt + 1 < tt1) load_x(tt + 1);
+    f32x4 acc[NJ][2];
+#pragma unroll
+    for (int n = 0; n < NJ; ++n)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) acc[n][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 xb[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        xb[hf] = *reinterpret_cast<const u32x4 *>(smem + buf * kXElems + (hf * 16 + l16) * kXS +
+                                                  ks * 32 + lq * 8);
+#pragma unroll
+      for (int n = 0; n < NJ; ++n)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          acc[n][hf] = M16::mma(as_v8<T>(wa[n][ks]), as_v8<T>(xb[hf]), acc[n][hf]);
+    }
+    // lane: columns wave*16NJ + 16n + 4lq + r of token 16hf + l16
+#pragma unroll
+    for (int n = 0; n < NJ; ++n)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        T4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(acc[n][hf][r]);
+        *reinterpret_cast<T4 *>(ystage + (hf * 16 + l16) * kYS + wave * 16 * NJ + n * 16 +
+                                lq * 4) = o;
+      }
+    __syncthreads();  // Y block staged; every wave is done with X buffer buf
+#pragma unroll
+    for (int i = 0; i < kRgTok * kYCh / 256; ++i) {
+      const int idx = i * 256 + tid, r = idx / kYCh, c = idx % kYCh;
+      const int64_t t = tt * kRgTok + r;
+      if (t < T_q && c * 8 < jn)
+        *reinterpret_cast<u32x4 *>(Y + t * ldy + g * ys + jb * kJB + c * 8) =
+            *reinterpret_cast<const u32x4 *>(ystage + r * kYS + c * 8);
+    }
+    if (tt + 1 < tt1) store_x(buf ^ 1);
+    __syncthreads();  // next X tile visible; the Y block is read out
+  }
+}
+
 // Weight gradient of a projection on 16-bit matrix cores, one workgroup per
 // (token chunk c, group g, 32-column block of d):
 //   part[c, f, g, d] = sum_{t in chunk c} A[t, g, f] B[t, g, d]
@@ -300,11 +418,25 @@ __global__ __launch_bounds__(256) void transpose2d_kernel(const T *__restrict__ 
   dst[i] = src[(int64_t)r * C + c];
 }
 
+// Workgroups of the tile-walking row GEMM: about this many in all.
+constexpr int64_t kRgTargetWgs = 512;
+
 template <typename T, int NJ, int KS>
 void rowgemm_nj(const RowGemm &p, hipStream_t st) {
   const int n_jb = (p.J + 64 * NJ - 1) / (64 * NJ);
-  const int64_t wgs = (p.T_q + kRgTok - 1) / kRgTok * p.G * n_jb;
-  if (wgs == 0) return;
+  const int64_t n_tt = (p.T_q + kRgTok - 1) / kRgTok;
+  if (n_tt == 0) return;
+  if (p.K <= 256) {
+    const int64_t units = n_tt * p.G * n_jb;
+    int64_t tpw = units / kRgTargetWgs;
+    tpw = tpw < 1 ? 1 : (tpw > 16 ? 16 : tpw);
+    const int64_t wgs = (n_tt + tpw - 1) / tpw * p.G * n_jb;
+    hipLaunchKernelGGL((rowgemm_tiles_kernel<T, NJ, KS>), dim3((unsigned)wgs), dim3(256), 0, st,
+                       (const T *)p.X, (const T *)p.W, (T *)p.Y, p.T_q, p.G, p.J, p.K, p.ldx,
+                       p.xs, p.ws, p.ldw, p.ldy, p.ys, n_jb, (int)tpw, n_tt);
+    return;
+  }
+  const int64_t wgs = n_tt * p.G * n_jb;
   hipLaunchKernelGGL((rowgemm_nt_kernel<T, NJ, KS>), dim3((unsigned)wgs), dim3(256), 0, st,
                      (const T *)p.X, (const T *)p.W, (T *)p.Y, p.T_q, p.G, p.J, p.K, p.ldx, p.xs,
                      p.ws, p.ldw, p.ldy, p.ys, n_jb);

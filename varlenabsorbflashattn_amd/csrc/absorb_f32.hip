@@ -572,6 +572,97 @@ void launch_bwd_fp(const AbsorbArgs &a, hipStream_t st) {
 // The fp32 matrix-core path takes H | 64 with H <= 8, D_KV a multiple of 4 up
 // to 256 (padded to a multiple of 64 inside the kernels) and D_H a multiple
 // of 16 up to 256.
+namespace {
+
+// dAX[t,h,f] = sum_d dO[t,h,d] W_V[f,h,d] in fp32 (ta/kernels.py:474-476, an
+// IEEE dot there): one wave per (32 tokens, head, 64 f) on 16x16x4 fp32
+// products, C[token][f] accumulated over 32-wide d blocks.  The reduction
+// order is relabelled (k step ks, slot l/16 <-> d = 32*blk + 8*(l/16) + ks) so
+// every operand comes from two contiguous 16-byte loads per lane: dO rows (A)
+// and W_V rows (B).  The wave's [32, 64] block is staged in LDS and written
+// as 16-byte row runs.
+__global__ __launch_bounds__(64) void absorb_dax_f32_kernel(const float *__restrict__ dO,
+                                                            const float *__restrict__ wv,
+                                                            float *__restrict__ dax, int64_t T_q,
+                                                            int H, int F, int DH) {
+  const int lane = threadIdx.x, l16 = lane & 15, lq = lane >> 4;
+  const int nfg = (F + 63) / 64;
+  int64_t w = blockIdx.x;
+  const int fg = (int)(w % nfg);
+  w /= nfg;
+  const int h = (int)(w % H);
+  const int64_t t0 = (w / H) * 32;
+  const int f0 = fg * 64;
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) acc[hf][ft] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < DH; db += 32) {
+    const int d = db + 8 * lq;
+    float a[2][8], b[4][8];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int64_t t = t0 + hf * 16 + l16;
+      const bool ok = t < T_q && d < DH;
+      const float *src = dO + (ok ? (t * H + h) * DH + d : 0);
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(src);
+      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[hf][e] = ok ? x0[e] : 0.f;
+        a[hf][4 + e] = ok ? x1[e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) {
+      const int f = f0 + ft * 16 + l16;
+      const bool ok = f < F && d < DH;
+      const float *src = wv + (ok ? ((int64_t)f * H + h) * DH + d : 0);
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(src);
+      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b[ft][e] = ok ? x0[e] : 0.f;
+        b[ft][4 + e] = ok ? x1[e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int ft = 0; ft < 4; ++ft) acc[hf][ft] = mma4(a[hf][ks], b[ft][ks], acc[hf][ft]);
+  }
+  // C: token 16*hf + 4*lq + r, f = f0 + 16*ft + l16
+  __shared__ __align__(16) float st[32][64 + 4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[hf * 16 + 4 * lq + r][ft * 16 + l16] = acc[hf][ft][r];
+  __syncthreads();
+  const int rr = lane >> 4, cc = (lane & 15) * 4;
+  if (f0 + cc < F)
+    for (int tk = rr; tk < 32; tk += 4) {
+      const int64_t t = t0 + tk;
+      if (t < T_q)
+        *reinterpret_cast<f32x4 *>(dax + (t * H + h) * F + f0 + cc) =
+            *reinterpret_cast<const f32x4 *>(&st[tk][cc]);
+    }
+}
+
+}  // namespace
+
+void launch_f32_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
+  const int64_t waves = (a.T_q + 31) / 32 * a.H * ((a.F + 63) / 64);
+  if (waves == 0) return;
+  hipLaunchKernelGGL(absorb_dax_f32_kernel, dim3((unsigned)waves), dim3(64), 0, st,
+                     (const float *)a.dO, (const float *)a.wv, (float *)a.dax, a.T_q, a.H, a.F,
+                     a.DH);
+}
+
 bool f32_absorb_supported(int H, int F, int DH) {
   return H >= 1 && H <= 8 && kAbsorbRows % H == 0 && F >= 4 && F % 4 == 0 && F <= 256 &&
          DH >= 16 && DH % 16 == 0 && DH <= 256;

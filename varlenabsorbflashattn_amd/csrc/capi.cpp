@@ -247,7 +247,10 @@ void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) dax_done = launch_mfma_absorb_dax<T>(a, st);
   if (!dax_done) {
     launch_row_dot<T>(a.O_in, a.dO, a.delta, a.T_q * a.H, a.DH, st);
-    launch_absorb_dax<T>(a, st);
+    if (sizeof(T) == 4 && f32_absorb_supported(a.H, a.F, a.DH))
+      launch_f32_absorb_dax(a, st);
+    else
+      launch_absorb_dax<T>(a, st);
   }
   if (mfma) {
     if constexpr (sizeof(T) == 2) {

@@ -144,6 +144,8 @@ template <typename T> void launch_mfma_absorb_dx(const AbsorbArgs &, hipStream_t
 bool f32_absorb_supported(int H, int F, int DH);
 int64_t f32_absorb_wvt_elems(int H, int F, int DH);
 void launch_f32_absorb_fwd(const AbsorbArgs &, hipStream_t);
+// dAX = dO W_V^T in fp32 on fp32 matrix cores (F % 4 == 0, D_H % 16 == 0)
+void launch_f32_absorb_dax(const AbsorbArgs &, hipStream_t);
 // du / aX (query side) and dX (key side); dAX and delta must be in the workspace
 void launch_f32_absorb_du_dx(const AbsorbArgs &, hipStream_t);
 

@@ -57,8 +57,8 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
   const int nt = (k1 - k0 + kBK - 1) / kBK;
 
   auto issue = [&](int kb, int buf) {
-    const int rows = k1 - kb < kBK ? (k1 - kb > 0 ? k1 - kb : 0) : kBK;
-    dma_block<FP, kDuWaves, S::XS>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
+    const int rows = uniform_clamp(k1 - kb, kBK);
+    dma_block<FP, kDuWaves, S::XS>(X + (int64_t)kb * F, (uint32_t)(rows * F * 2), F,
                             lds_addr(smem + buf * S::kTile), wave, lane);
   };
 #pragma unroll
@@ -241,13 +241,13 @@ struct DxItem {
   __device__ void issue(int blk, int buf) const {
     unsigned char *base = smem + buf * S::kBufBytes;
     const int rb = r0 + blk * 32;
-    const int rows = r1 - rb < 32 ? r1 - rb : 32;
-    const int64_t nb = (int64_t)rows * F * 2;
+    const int rows = uniform_clamp(r1 - rb, 32);
+    const uint32_t nb = (uint32_t)(rows * F * 2);
     dma_block<FP, kDxWaves, XS>(u + (int64_t)rb * F, nb, F, lds_addr(base), wave, lane);
     dma_block<FP, kDxWaves, XS>(dax + (int64_t)rb * F, nb, F, lds_addr(base + S::kBlk * 2), wave,
                             lane);
     const float *vec = (wave & 1) ? delta : lse;
-    const u32x4 rv = rsrc_words(vec + rb, (int64_t)rows * 4);
+    const u32x4 rv = rsrc_words32(vec + rb, (uint32_t)(rows * 4));
     if (lane < 8) lds_dma16(rv, lds_addr(base + 2 * S::kBlk * 2 + (wave & 1) * 128), lane * 16);
   }
 

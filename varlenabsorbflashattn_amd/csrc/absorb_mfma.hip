@@ -79,8 +79,8 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   const int nt = (k1 - k0 + kBK - 1) / kBK;
 
   auto issue = [&](int kb, int buf) {
-    const int rows = k1 - kb < kBK ? (k1 - kb > 0 ? k1 - kb : 0) : kBK;
-    dma_block<FP, kFwdWaves, S::XS>(X + (int64_t)kb * F, (int64_t)rows * F * 2, F,
+    const int rows = uniform_clamp(k1 - kb, kBK);
+    dma_block<FP, kFwdWaves, S::XS>(X + (int64_t)kb * F, (uint32_t)(rows * F * 2), F,
                              lds_addr(smem + buf * S::kTile), wave, lane);
   };
 #pragma unroll

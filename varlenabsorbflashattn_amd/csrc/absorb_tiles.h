@@ -54,9 +54,9 @@ struct Mfma16<f16> {
 // not hoist the rows' offsets into separate registers.  Chunks past F carry an
 // offset of 2^31 and read as zeros.
 template <int FP, int NW, int XS>
-__device__ __forceinline__ void dma_block(const void *src, int64_t bytes, int F, uint32_t base,
+__device__ __forceinline__ void dma_block(const void *src, uint32_t bytes, int F, uint32_t base,
                                           int wave, int lane) {
-  const u32x4 rs = rsrc_words(src, bytes);
+  const u32x4 rs = rsrc_words32(src, bytes);
   const uint32_t off = lane < F / 8 ? (uint32_t)lane * 16u : 0x80000000u;
   if (lane < FP / 8) {
 #pragma unroll

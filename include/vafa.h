@@ -136,7 +136,9 @@ VAFA_API int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t 
 /* returns, 256-byte aligned.  stream: hipStream_t.                          */
 /* ======================================================================== */
 
-/* Workspace bytes needed by vafa_varlen_fwd / vafa_varlen_bwd. */
+/* Workspace bytes needed by vafa_varlen_fwd / vafa_varlen_bwd.  For D=16 this
+ * includes zero-padded D=32 copies of the operands: 16-bit D=16 calls run on
+ * the D=32 matrix-core kernels over them (fp32 calls leave them unused). */
 VAFA_API int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D);
 VAFA_API int64_t vafa_varlen_bwd_workspace(const vafa_plan_info *info, int64_t D);
 

@@ -27,6 +27,10 @@ CASES = [
     ("head_dim_32", [70, 5], [90, 200], 32),
     ("head_dim_256", [130, 3], [77, 300], 256),
     ("head_dim_16", [33, 9], [40, 70], 16),
+    # D=16 runs on the D=32 matrix-core kernels over zero-padded copies:
+    # split-K partials and the fused key-major backward at that width
+    ("head_dim_16_split", [3, 40, 129], [5000, 9000, 130], 16),
+    ("head_dim_16_fused", [16, 5, 1], [3000, 700, 64], 16),
     ("empty_segments", [0, 5, 9, 0], [3, 0, 40, 7], 64),
     ("long_split", [150, 20], [9000, 5000], 64),
     ("decode_split", [3, 16, 1], [3000, 1500, 1024], 128),

@@ -63,17 +63,41 @@ bool supported_d(int64_t D) {
 // ---- varlen ---------------------------------------------------------------
 struct VarlenWs {
   float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *part_fq = nullptr;
+  // D=16 on the matrix cores: zero-padded D=32 copies of the operands
+  void *pq = nullptr, *pk = nullptr, *pv = nullptr, *po = nullptr, *pdo = nullptr,
+       *pdq = nullptr, *pdk = nullptr, *pdv = nullptr;
   int64_t bytes = 0;
 };
 
-VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd) {
+// D=16 with 16-bit operands runs on the D=32 matrix-core kernels over
+// zero-padded copies (the zero columns add exact zeros to every product; the
+// caller's scale is kept); fp32 D=16 stays on the wave-per-row kernels.
+inline bool pad_d16(int64_t D, int32_t dtype) {
+  return D == 16 && (dtype == VAFA_BF16 || dtype == VAFA_F16);
+}
+
+VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd, bool pad) {
   Carver c(ws);
   VarlenWs w;
+  const int64_t Dc = pad ? 32 : D;
   const int64_t rows = info->n_part_rows * info->H;
   if (bwd) w.delta = c.take<float>(info->T_q * info->H * 4);
-  w.part_o = c.take<float>(rows * D * 4);
+  w.part_o = c.take<float>(rows * Dc * 4);
   if (!bwd) w.part_lse = c.take<float>(rows * 4);
-  if (bwd) w.part_fq = c.take<float>(info->n_fpart_rows * info->H * D * 4);
+  if (bwd) w.part_fq = c.take<float>(info->n_fpart_rows * info->H * Dc * 4);
+  if (pad) {
+    const int64_t nq = info->T_q * info->H * 32 * 2, nk = info->T_k * info->H * 32 * 2;
+    w.pq = c.take<void>(nq);
+    w.pk = c.take<void>(nk);
+    w.pv = c.take<void>(nk);
+    w.po = c.take<void>(nq);
+    if (bwd) {
+      w.pdo = c.take<void>(nq);
+      w.pdq = c.take<void>(nq);
+      w.pdk = c.take<void>(nk);
+      w.pdv = c.take<void>(nk);
+    }
+  }
   w.bytes = c.used;
   return w;
 }
@@ -440,27 +464,31 @@ extern "C" {
 
 const char *vafa_version(void) { return "vafa 0.1.0 gfx950"; }
 
+// The workspace functions do not see the dtype: for D=16 they include the
+// padded copies, which only 16-bit calls use.
 int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D) {
   if (check_info(info, 1)) return -1;
-  return carve_varlen(nullptr, info, D, false).bytes;
+  return carve_varlen(nullptr, info, D, false, D == 16).bytes;
 }
 
 int64_t vafa_varlen_bwd_workspace(const vafa_plan_info *info, int64_t D) {
   if (check_info(info, 1)) return -1;
-  return carve_varlen(nullptr, info, D, true).bytes;
+  return carve_varlen(nullptr, info, D, true, D == 16).bytes;
 }
 
-int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
-                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
-                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
-                    void *stream) {
+static int varlen_fwd_impl(const void *q, const void *k, const void *v, void *o, float *lse,
+                           const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                           int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                           void *stream, bool allow_pad) {
   if (int rc = check_info(info, 1)) return rc;
   if (!supported_d(D))
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
-  VarlenWs w = carve_varlen(workspace, info, D, false);
+  const bool pad = allow_pad && pad_d16(D, dtype);
+  VarlenWs w = carve_varlen(workspace, info, D, false, pad);
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
     return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
                 (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
   VarlenArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
   a.part_o = w.part_o; a.part_lse = w.part_lse;
@@ -469,8 +497,23 @@ int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float 
   a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
-  if (int rc = by_dtype<VFwd>(dtype, a, (hipStream_t)stream)) return rc;
+  if (pad) {
+    launch_pad16(q, w.pq, info->T_q * info->H, st);
+    launch_pad16(k, w.pk, info->T_k * info->H, st);
+    launch_pad16(v, w.pv, info->T_k * info->H, st);
+    a.q = w.pq; a.k = w.pk; a.v = w.pv; a.o = w.po; a.D = 32;
+  }
+  if (int rc = by_dtype<VFwd>(dtype, a, st)) return rc;
+  if (pad) launch_unpad16(w.po, o, info->T_q * info->H, st);
   return check_launch("vafa_varlen_fwd");
+}
+
+int vafa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                    const int32_t *plan_dev, const vafa_plan_info *info, int64_t D,
+                    int32_t dtype, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream) {
+  return varlen_fwd_impl(q, k, v, o, lse, plan_dev, info, D, dtype, scale, workspace,
+                         workspace_bytes, stream, true);
 }
 
 int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o, float *lse,
@@ -479,7 +522,9 @@ int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o
   if (int rc = check_info(info, 1)) return rc;
   if (!supported_d(D))
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
-  const int64_t need = carve_varlen(nullptr, info, D, false).bytes;
+  // D=16 stays on the wave-per-row kernels here: the static scratch holds
+  // the split partials only, not padded operand copies
+  const int64_t need = carve_varlen(nullptr, info, D, false, false).bytes;
   if (need > kScratchBytes)
     return fail(VAFA_ERR_WORKSPACE,
                 "vafa_varlen_fwd_noalloc: this plan's split partials need %lld bytes, the "
@@ -489,8 +534,8 @@ int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o
   if (need > 0) {
     if (int rc = scratch_ptr(&ws)) return rc;
   }
-  return vafa_varlen_fwd(q, k, v, o, lse, plan_dev, info, D, dtype, scale, ws,
-                         need > 0 ? kScratchBytes : 0, stream);
+  return varlen_fwd_impl(q, k, v, o, lse, plan_dev, info, D, dtype, scale, ws,
+                         need > 0 ? kScratchBytes : 0, stream, false);
 }
 
 static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const void *v,
@@ -503,10 +548,14 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
   if (stage < -1 || stage > VAFA_BWD_DKV)
     return fail(VAFA_ERR_VALUE, "unknown backward stage %d", (int)stage);
-  VarlenWs w = carve_varlen(workspace, info, D, true);
+  // the stage entry points (a test and profiling API) keep D=16 on the
+  // wave-per-row kernels
+  const bool pad = stage < 0 && pad_d16(D, dtype);
+  VarlenWs w = carve_varlen(workspace, info, D, true, pad);
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
     return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
                 (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
   VarlenArgs a{};
   a.q = q; a.k = k; a.v = v; a.o_in = o; a.dout = dout; a.lse_in = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
@@ -523,9 +572,23 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   a.stage = stage;
-  const int rc = stage < 0 ? by_dtype<VBwd>(dtype, a, (hipStream_t)stream)
-                           : by_dtype<VBwdStage>(dtype, a, (hipStream_t)stream);
+  if (pad) {
+    const int64_t rq = info->T_q * info->H, rk = info->T_k * info->H;
+    launch_pad16(q, w.pq, rq, st);
+    launch_pad16(k, w.pk, rk, st);
+    launch_pad16(v, w.pv, rk, st);
+    launch_pad16(o, w.po, rq, st);
+    launch_pad16(dout, w.pdo, rq, st);
+    a.q = w.pq; a.k = w.pk; a.v = w.pv; a.o_in = w.po; a.dout = w.pdo;
+    a.dq = w.pdq; a.dk = w.pdk; a.dv = w.pdv; a.D = 32;
+  }
+  const int rc = stage < 0 ? by_dtype<VBwd>(dtype, a, st) : by_dtype<VBwdStage>(dtype, a, st);
   if (rc) return rc;
+  if (pad) {
+    launch_unpad16(w.pdq, dq, info->T_q * info->H, st);
+    launch_unpad16(w.pdk, dk, info->T_k * info->H, st);
+    launch_unpad16(w.pdv, dv, info->T_k * info->H, st);
+  }
   return check_launch("vafa_varlen_bwd");
 }
 

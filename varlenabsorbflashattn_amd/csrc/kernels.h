@@ -86,6 +86,9 @@ void launch_absorb_dwv(const AbsorbArgs &, hipStream_t);
 template <typename TA, typename T>
 void launch_wgrad(const void *a, const void *b, float *part, void *out, int64_t T_q,
                   int64_t tchunk, int64_t n_chunks, int G, int F, int DH, hipStream_t);
+// 16-bit rows [rows, 16] -> zero-padded [rows, 32], and the first 16 columns back
+void launch_pad16(const void *src, void *dst, int64_t rows, hipStream_t);
+void launch_unpad16(const void *src, void *dst, int64_t rows, hipStream_t);
 // out[o] = sum_c part[c * n_out + o] in chunk order, rounded to T
 template <typename T>
 void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chunks, hipStream_t);

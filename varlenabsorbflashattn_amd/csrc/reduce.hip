@@ -433,6 +433,29 @@ __global__ __launch_bounds__(256) void absorb_dwv_sum_kernel(const float *__rest
   dwv[o] = from_f<T>(s);
 }
 
+// [rows, 16] -> [rows, 32] with zero columns 16..31, and back: D=16 runs on
+// the D=32 matrix-core kernels (16-bit elements, 16-byte chunks).
+__global__ __launch_bounds__(256) void pad16_kernel(const uint16_t *__restrict__ src,
+                                                    uint16_t *__restrict__ dst, int64_t rows) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * 4) return;
+  const int64_t r = i >> 2;
+  const int c = (int)(i & 3);
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (c < 2) v = *reinterpret_cast<const u32x4 *>(src + r * 16 + c * 8);
+  *reinterpret_cast<u32x4 *>(dst + r * 32 + c * 8) = v;
+}
+
+__global__ __launch_bounds__(256) void unpad16_kernel(const uint16_t *__restrict__ src,
+                                                      uint16_t *__restrict__ dst, int64_t rows) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * 2) return;
+  const int64_t r = i >> 1;
+  const int c = (int)(i & 1);
+  *reinterpret_cast<u32x4 *>(dst + r * 16 + c * 8) =
+      *reinterpret_cast<const u32x4 *>(src + r * 32 + c * 8);
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -530,6 +553,18 @@ void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
   }
   launch_wgrad<float, T>(a.ax, a.dO, a.dwv_part, a.dwv, a.T_q, a.tchunk, a.n_tchunks, a.H, a.F,
                          a.DH, st);
+}
+
+void launch_pad16(const void *src, void *dst, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(pad16_kernel, dim3(blocks_for(rows * 4)), dim3(256), 0, st,
+                     (const uint16_t *)src, (uint16_t *)dst, rows);
+}
+
+void launch_unpad16(const void *src, void *dst, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(unpad16_kernel, dim3(blocks_for(rows * 2)), dim3(256), 0, st,
+                     (const uint16_t *)src, (uint16_t *)dst, rows);
 }
 
 #define VAFA_INST(T)                                                                        \

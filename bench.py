@@ -12,7 +12,7 @@ and max over its timed iterations, each bracketed by HIP events (the
 reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d256,fused,copy,replay}
+       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d16,d256,fused,copy,replay}
 """
 from __future__ import annotations
 
@@ -465,6 +465,11 @@ def run_only(which, steps, warmup):
         line = varlen_line(case, step_st, fwd_st)
         line["bwd_GB/s"] = fused_bwd_bytes(case) / ((step_st["mean"] - fwd_st["mean"]) * 1e-3) / 1e9
         return {"config": case.name, **line}
+    if which == "d16":
+        c = W.config2(seed=0)
+        case = W.VarlenCase("c2_lengths_H16_D16", c.q_lens, c.k_lens, 16, 16, torch.bfloat16)
+        step_st, fwd_st = bench_varlen_case(case, max(steps, 3), warmup)
+        return {"config": case.name, **varlen_line(case, step_st, fwd_st)}
     if which == "d256":
         c = W.config2(seed=0)
         case = W.VarlenCase("c2_lengths_H8_D256", c.q_lens, c.k_lens, 8, 256, torch.bfloat16)
@@ -501,7 +506,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c4full", "c5",
-                                       "d256", "fused", "copy", "replay"],
+                                       "d16", "d256", "fused", "copy", "replay"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -573,6 +578,12 @@ def main():
         s_st, f_st = bench_varlen_case(c256, n2, 3)
         secondary["varlen_d256_fwd_bwd"] = varlen_line(c256, s_st, f_st)
         log("D=256", s_st["mean"], f_st["mean"])
+        # D=16 (16-bit: the D=32 kernels over zero-padded copies) at C2's shape
+        c16 = W.VarlenCase("c2_lengths_H16_D16", case.q_lens, case.k_lens, 16, 16,
+                           torch.bfloat16)
+        s_st, f_st = bench_varlen_case(c16, n2, 3)
+        secondary["varlen_d16_fwd_bwd"] = varlen_line(c16, s_st, f_st)
+        log("D=16", s_st["mean"], f_st["mean"])
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     out = {
         "metric": "varlen-FA fwd/bwd TFLOP/s + absorb-attn HBM GB/s, % of MI355X peak",

@@ -26,6 +26,9 @@ CASES = [
     ("head_dim_128", [200, 300], [150, 250], 128),
     ("head_dim_32", [70, 5], [90, 200], 32),
     ("head_dim_256", [130, 3], [77, 300], 256),
+    # D=256 dK/dV runs as two workgroups per key tile (one half of d each):
+    # several key tiles, a key tail and a split-K forward
+    ("head_dim_256_long", [300, 17, 40], [700, 129, 5000], 256),
     ("head_dim_16", [33, 9], [40, 70], 16),
     # D=16 runs on the D=32 matrix-core kernels over zero-padded copies:
     # split-K partials and the fused key-major backward at that width

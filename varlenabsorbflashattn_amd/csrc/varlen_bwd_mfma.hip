@@ -91,9 +91,17 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   using S = DkvSmem<D>;
   constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
   constexpr int kPre = D >= 128 ? 2 : 4;  // operand ring depth within the register budget
+  // At D=256 two workgroups share a key tile, each accumulating dK/dV for one
+  // half of d (S and dP still over all of d): the full-width accumulators did
+  // not fit beside the K/V operands and spilled.
+  constexpr int kDsplit = D >= 256 ? 2 : 1;
+  constexpr int NDO = ND / kDsplit;  // 32-wide d tiles of dK/dV per workgroup
+  static_assert(!FQ || kDsplit == 1, "the fused variant keeps all of d");
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
-  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const int dpart = kDsplit > 1 ? (int)(blockIdx.x % kDsplit) : 0;
+  const int bid = blockIdx.x / kDsplit;
+  const int item = bid / H, h = bid % H;
   const PlanItem it = load_item(items, item);
   const int k0 = it.v[0], k1 = it.v[1], q0 = it.v[2], q1 = it.v[3];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -150,9 +158,9 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     }
   }
   const int pbase = FQ ? it.v[5] : 0;
-  f32x16 adk[ND], adv[ND];
+  f32x16 adk[NDO], adv[NDO];
 #pragma unroll
-  for (int i = 0; i < ND; ++i)
+  for (int i = 0; i < NDO; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) adk[i][r] = adv[i][r] = 0.f;
 
@@ -189,11 +197,12 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
         if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // transposed operands: i -> d tile i % ND, query half mm = (i / ND) >> 1,
-      // dO^T (for dV^T, with P) when (i / ND) is even, else Q^T (for dK^T, with dS)
+      // transposed operands: i -> this workgroup's d tile i % NDO, query half
+      // mm = (i / NDO) >> 1, dO^T (for dV^T, with P) when (i / NDO) is even,
+      // else Q^T (for dK^T, with dS)
       auto top = [&](int i) {
-        const lds_cptr<T> p =
-            (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
+        const lds_cptr<T> p = (((i / NDO) & 1) ? qs : ds_) + t_off +
+                              ((i / NDO) >> 1) * 16 * RS + (dpart * NDO + i % NDO) * 32;
         return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
       };
       typename M::v8 tring[kPre];
@@ -221,11 +230,11 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       }
       pb[0] = pack8<T>(s, 0);
       sb[0] = pack8<T>(dp, 0);
-      // the 8 second-half rows are spread over the first 2*ND products: kRowsPer
-      // rows at every kEvery-th product (one row every second product at D=256)
-      constexpr int kSteps = 2 * ND < 8 ? 2 * ND : 8;
+      // the 8 second-half rows are spread over the first 2*NDO products:
+      // kRowsPer rows at every kEvery-th product
+      constexpr int kSteps = 2 * NDO < 8 ? 2 * NDO : 8;
       constexpr int kRowsPer = 8 / kSteps;
-      constexpr int kEvery = 2 * ND / kSteps;
+      constexpr int kEvery = 2 * NDO / kSteps;
       auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
       auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
       float Ln[kRowsPer], Dn[kRowsPer];
@@ -233,15 +242,15 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       for (int rr = 0; rr < kRowsPer; ++rr) Ln[rr] = lse_at(8 + rr), Dn[rr] = del_at(8 + rr);
       __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
-      for (int i = 0; i < 4 * ND; ++i) {
-        const int dt = i % ND, q2 = i / ND, mm = q2 >> 1;
+      for (int i = 0; i < 4 * NDO; ++i) {
+        const int dt = i % NDO, q2 = i / NDO, mm = q2 >> 1;
         const typename M::v8 a = tring[i % kPre];
         if (q2 & 1)
           adk[dt] = M::mma(a, sb[mm], adk[dt]);
         else
           adv[dt] = M::mma(a, pb[mm], adv[dt]);
-        if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
-        if (i < 2 * ND && i % kEvery == 0) {
+        if (i + kPre < 4 * NDO) tring[i % kPre] = top(i + kPre);
+        if (i < 2 * NDO && i % kEvery == 0) {
           const int g = i / kEvery;
           float Lc[kRowsPer], Dc[kRowsPer];
   #pragma unroll
@@ -338,7 +347,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   T *dkr = dk + ((int64_t)key * H + h) * D;
   T *dvr = dv + ((int64_t)key * H + h) * D;
 #pragma unroll
-  for (int dtile = 0; dtile < ND; ++dtile)
+  for (int dtile = 0; dtile < NDO; ++dtile)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       T4 wk, wv;
@@ -347,7 +356,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
         wk[e] = static_cast<T>(adk[dtile][g * 4 + e] * scale);
         wv[e] = static_cast<T>(adv[dtile][g * 4 + e]);
       }
-      const int d = dtile * 32 + g * 8 + lhalf * 4;
+      const int d = (dpart * NDO + dtile) * 32 + g * 8 + lhalf * 4;
       *reinterpret_cast<T4 *>(dkr + d) = wk;
       *reinterpret_cast<T4 *>(dvr + d) = wv;
     }
@@ -596,7 +605,9 @@ void launch_mfma_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   const int smem = DkvSmem<D>::kBytes;
   hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, false>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false>), dim3((unsigned)(a.n_kv * a.H)), dim3(256),
+  const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false>), dim3((unsigned)(a.n_kv * a.H * dsplit)),
+                     dim3(256),
                      smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
                      a.scale * kLog2e, a.scale, nullptr);

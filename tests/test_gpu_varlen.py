@@ -80,10 +80,13 @@ def test_varlen_bf16_parity(device, name, q_lens, k_lens, D):
         assert_close(n, a, r)
 
 
+@pytest.mark.parametrize("D", [64, 16])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
-def test_varlen_other_dtypes(device, dtype):
-    print(f"[varlen {dtype}]", flush=True)
-    got, ref = run_case([17, 64, 128, 200], [17, 64, 128, 200], 4, 64, dtype, device)
+def test_varlen_other_dtypes(device, dtype, D):
+    """fp16 (matrix cores; at D=16 over zero-padded D=32 copies) and fp32 (the
+    wave-per-row kernels)."""
+    print(f"[varlen {dtype}] D={D}", flush=True)
+    got, ref = run_case([17, 64, 128, 200], [17, 64, 128, 200], 4, D, dtype, device)
     for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
         assert_close(n, a, r)
 

@@ -180,8 +180,10 @@ def check_varlen_plan(q_lens, k_lens, H=4, D=64):
     fused = (lq > 0) & (lq <= 16) & (np.diff(ck) >= 1) & (D <= 64)
     fkv, fcomb = p.section("fkv"), p.section("fcomb")
     keys = np.zeros(int(ck[-1]), dtype=np.int64)
+    BK = p.info.k_tile
     for k0, k1, q0, q1, seg, *_ in kv.tolist():
         assert (q0, q1) == (cq[seg], cq[seg + 1]) and not fused[seg]
+        assert (k0 - ck[seg]) % BK == 0 and 0 < k1 - k0 <= BK
         keys[k0:k1] += 1
     for k0, k1, q0, q1, seg, *_ in fkv.tolist():
         assert (q0, q1) == (cq[seg], cq[seg + 1]) and fused[seg]
@@ -224,13 +226,51 @@ def test_varlen_plan_small_cases():
             check_varlen_plan(ql, kl, D=D)
 
 
+def expected_tiles(q_lens, k_lens, D):
+    """256-row query tiles for D <= 128 and 256-key tiles for D = 128 when at
+    least half of the work (sum of Lq * Lk) lies in segments longer than 128
+    queries (keys); 128 otherwise."""
+    lq, lk = np.asarray(q_lens, dtype=np.float64), np.asarray(k_lens, dtype=np.float64)
+    w = lq * lk
+    work = w.sum()
+    q = 256 if D <= 128 and work > 0 and 2 * w[lq > 128].sum() >= work else 128
+    k = 256 if D == 128 and work > 0 and 2 * w[lk > 128].sum() >= work else 128
+    return q, k
+
+
+@pytest.mark.parametrize("q_lens,k_lens", [
+    ([200, 300], [150, 250]),        # long segments: wide tiles at D <= 128 / D = 128
+    ([3, 16, 1], [5000, 900, 40]),   # decode-shaped: 128-row tiles, 256-key tiles at D=128
+    ([100, 129], [100, 129]),        # 129 * 129 > 100 * 100: the longer segment decides
+    ([129, 100, 100], [10, 200, 200]),
+    ([0, 0], [5, 7]),                # no work: narrow tiles
+    ([300], [64]),                   # long queries, short keys
+])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_varlen_tile_choice(q_lens, k_lens, D):
+    p = check_varlen_plan(q_lens, k_lens, H=2, D=D)
+    assert (p.info.q_tile, p.info.k_tile) == expected_tiles(q_lens, k_lens, D)
+
+
+def test_varlen_tile_choice_on_configs():
+    from varlenabsorbflashattn_amd import workloads as W
+    c2, c3 = W.config2(0), W.config3(0)
+    assert expected_tiles(c2.q_lens, c2.k_lens, c2.D) == (256, 256)
+    assert expected_tiles(c3.q_lens, c3.k_lens, c3.D) == (128, 256)
+
+
 def test_varlen_plan_split_counts_match_reference_rule():
     # prefill-like tiles split ceil(Lk/4096) ways like fa/chunk_indices.py:172-287
+    # (per query tile of the plan's height)
     ql, kl = [300, 200, 40], [9000, 4096, 70000]
-    p = check_varlen_plan(ql, kl)
-    _, split, comb = meta.split_plan(_cu(ql), _cu(kl), 128, 4096, 4096)
-    assert p.info.n_comb == comb.shape[0]
-    assert p.info.n_fwd - (3 + 2 + 1 - comb.shape[0]) == split.shape[0]
+    for D in (64, 256):  # 256-row tiles at D=64, 128-row tiles at D=256
+        p = check_varlen_plan(ql, kl, D=D)
+        BM = int(p.info.q_tile)
+        assert BM == (256 if D == 64 else 128)
+        _, split, comb = meta.split_plan(_cu(ql), _cu(kl), BM, 4096, 4096)
+        n_tiles = sum(-(-q // BM) for q in ql)
+        assert p.info.n_comb == comb.shape[0]
+        assert p.info.n_fwd - (n_tiles - comb.shape[0]) == split.shape[0]
 
 
 def test_varlen_plan_decode_split_range():

@@ -49,6 +49,23 @@ int check_info(const vafa_plan_info *info, int64_t kind) {
   return VAFA_OK;
 }
 
+// A varlen plan's tiles must be ones the kernels of this head dim run: the
+// planner picks 256-row query tiles only for D <= 128 and 256-key tiles only
+// for D = 128 (D=16 runs on the D=32 kernels).
+int check_varlen_tiles(const vafa_plan_info *info, int64_t D) {
+  const int64_t Dk = D == 16 ? 32 : D;
+  const bool q_ok =
+      info->q_tile == kVarlenTile || (info->q_tile == kVarlenWideTile && Dk <= 128);
+  const bool k_ok =
+      info->k_tile == kVarlenTile || (info->k_tile == kVarlenWideTile && Dk == 128);
+  if (!q_ok || !k_ok)
+    return fail(VAFA_ERR_VALUE,
+                "plan tiles (%lld queries, %lld keys) do not fit head_dim %lld: build the "
+                "plan with this head_dim",
+                (long long)info->q_tile, (long long)info->k_tile, (long long)D);
+  return VAFA_OK;
+}
+
 int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -483,6 +500,7 @@ static int varlen_fwd_impl(const void *q, const void *k, const void *v, void *o,
   if (int rc = check_info(info, 1)) return rc;
   if (!supported_d(D))
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
+  if (int rc = check_varlen_tiles(info, D)) return rc;
   const bool pad = allow_pad && pad_d16(D, dtype);
   VarlenWs w = carve_varlen(workspace, info, D, false, pad);
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
@@ -497,6 +515,7 @@ static int varlen_fwd_impl(const void *q, const void *k, const void *v, void *o,
   a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
+  a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
   if (pad) {
     launch_pad16(q, w.pq, info->T_q * info->H, st);
     launch_pad16(k, w.pk, info->T_k * info->H, st);
@@ -548,6 +567,7 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
     return fail(VAFA_ERR_ASSERT, "head_dim %lld not supported (try 64/128/256)", (long long)D);
   if (stage < -1 || stage > VAFA_BWD_DKV)
     return fail(VAFA_ERR_VALUE, "unknown backward stage %d", (int)stage);
+  if (int rc = check_varlen_tiles(info, D)) return rc;
   // the stage entry points (a test and profiling API) keep D=16 on the
   // wave-per-row kernels
   const bool pad = stage < 0 && pad_d16(D, dtype);
@@ -571,6 +591,7 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
+  a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
   a.stage = stage;
   if (pad) {
     const int64_t rq = info->T_q * info->H, rk = info->T_k * info->H;

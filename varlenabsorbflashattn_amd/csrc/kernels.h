@@ -19,6 +19,7 @@ struct VarlenArgs {
   int comb_rows;         // most rows of one combine item
   int64_t T_q;
   int H, D;
+  int q_tile, k_tile;  // the plan's tiles: forward / dQ rows and dK/dV keys per workgroup
   float scale;
   int stage;  // backward stage (VAFA_BWD_*) or -1 for all
   // the matrix-core dQ kernel computes delta from O and dO itself and writes

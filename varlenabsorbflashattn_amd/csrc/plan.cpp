@@ -68,6 +68,30 @@ void key_split(int64_t rows, int64_t lk, const SplitPolicy &p, int64_t *ns_out,
   *chunk_out = chunk;
 }
 
+// Query and key tiles of a varlen plan.  A 256-row query tile (8-wave
+// forward and dQ workgroups) shares every staged K/V tile among twice the
+// queries: it pays off when most of the work (sum of Lq * Lk) lies in
+// segments with more than 128 queries, and loses on decode-shaped batches,
+// where one active wave per workgroup halves the key streams in flight per CU.
+// 256-key dK/dV tiles pay off at D=128 (two waves per SIMD either way) when
+// most of the work lies in segments with more than 128 keys; at D <= 64 the
+// 4-wave kernel holds more waves per SIMD and stays.  Measured on the MI355X:
+// configs[1] forward -2%, dK/dV -2.5%; configs[2] forward +10% with 256-row
+// tiles; stage-1 replay (D=64) forward -6.6%, dK/dV +1.7% with 256-key tiles.
+void varlen_tiles(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t D, int64_t *bm,
+                  int64_t *bk) {
+  double work = 0.0, long_q = 0.0, long_k = 0.0;
+  for (int64_t s = 0; s + 1 < n1; ++s) {
+    const int64_t lq = cu_q[s + 1] - cu_q[s], lk = cu_k[s + 1] - cu_k[s];
+    const double w = (double)lq * (double)lk;
+    work += w;
+    if (lq > kVarlenTile) long_q += w;
+    if (lk > kVarlenTile) long_k += w;
+  }
+  *bm = D <= 128 && work > 0.0 && 2.0 * long_q >= work ? kVarlenWideTile : kVarlenTile;
+  *bk = D == 128 && work > 0.0 && 2.0 * long_k >= work ? kVarlenWideTile : kVarlenTile;
+}
+
 void sort_lpt(std::vector<Item> &items) {
   std::stable_sort(items.begin(), items.end(),
                    [](const Item &a, const Item &b) { return a.cost > b.cost; });
@@ -279,7 +303,8 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
   int rc = check_pair(cu_q, cu_k, n1);
   if (rc) return rc;
   const SplitPolicy &pol = kVarlenPolicy;
-  const int64_t BM = kVarlenQTile, BK = kVarlenKTile;
+  int64_t BM = kVarlenTile, BK = kVarlenTile;
+  varlen_tiles(cu_q, cu_k, n1, D, &BM, &BK);
   std::memset(info, 0, sizeof(*info));
   info->magic = VAFA_PLAN_MAGIC;
   info->kind = 1;
@@ -319,9 +344,11 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
       }
       prow += ns * rows;
     }
-    const int64_t ntiles = (lk + BK - 1) / BK;
-    for (int64_t k = k0, j = 0; k < k1; k += BK, ++j) {
-      const int64_t ke = std::min(k + BK, k1);
+    // fused segments (D <= 64, so BK is kVarlenTile there too) keep 128-key tiles
+    const int64_t bk = fused[s] ? kVarlenTile : BK;
+    const int64_t ntiles = (lk + bk - 1) / bk;
+    for (int64_t k = k0, j = 0; k < k1; k += bk, ++j) {
+      const int64_t ke = std::min(k + bk, k1);
       if (fused[s]) {
         fkv.push_back(Item{{(int32_t)k, (int32_t)ke, (int32_t)q0, (int32_t)q1, (int32_t)s,
                             (int32_t)(fprow + j * lq), (int32_t)j, (int32_t)ntiles},

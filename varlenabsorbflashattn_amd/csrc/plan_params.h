@@ -4,10 +4,13 @@
 
 namespace vafa {
 
-// Varlen: a forward / dQ workgroup covers kVarlenQTile query rows (4 waves x 32
-// rows); a dK/dV workgroup covers kVarlenKTile keys (4 waves x 32 keys).
-constexpr int kVarlenQTile = 128;
-constexpr int kVarlenKTile = 128;
+// Varlen: a forward / dQ workgroup covers one query tile (32 rows per wave)
+// and a dK/dV workgroup one key tile (32 keys per wave).  The planner picks
+// each per call between kVarlenTile (4-wave workgroups) and kVarlenWideTile
+// (8-wave workgroups, D <= 128 only: at D=256 one wave per SIMD holds the
+// registers); the fused K-major pass always uses kVarlenTile keys.
+constexpr int kVarlenTile = 128;
+constexpr int kVarlenWideTile = 256;
 // Absorb: a forward workgroup covers up to kAbsorbRows (token, head) rows;
 // a dX workgroup covers up to kAbsorbKTile keys of one sample (four 128-key
 // sub-tiles on the matrix-core path).

@@ -2,9 +2,10 @@
 //
 // Two deterministic kernels (no atomics), both recomputing P = exp2(S*c - LSE)
 // from the forward's log2-domain LSE (fa/kernels.py:233-494):
-//   * dK/dV, key-major: a workgroup owns 128 keys of one head (32 per wave,
-//     K and V held in registers as MFMA operands) and walks the segment's
-//     queries in blocks of 32 staged row-major in LDS by buffer_load ... lds,
+//   * dK/dV, key-major: a workgroup owns the plan's key tile (128 or 256 keys)
+//     of one head (32 per wave, K and V held in registers as MFMA operands)
+//     and walks the segment's queries in blocks of 32 staged row-major in LDS
+//     by buffer_load ... lds,
 //     double-buffered (the transposed operands Q^T, dO^T come from
 //     ds_read_b64_tr_b16):
 //       S = Q K^T, dP = dO V^T, dS = P (dP - delta),
@@ -60,29 +61,31 @@ struct FqSmem {
 };
 
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
-// past r_end read as zero) into a padded [32][RS] block: wave w moves rows
-// 8w .. 8w+7, one instruction per row with lanes < D/8 active.  One buffer
-// descriptor covers the block's valid rows; the row sits in the lane offset.
-template <typename T, int D>
+// past r_end read as zero) into a padded [32][RS] block: wave w of NW moves
+// rows RPW*w .. RPW*w + RPW-1 (RPW = 32/NW), one instruction per row with
+// lanes < D/8 active.  One buffer descriptor covers the block's valid rows;
+// the row sits in the lane offset.
+template <typename T, int D, int NW>
 __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
                                          uint32_t base, int wave, int lane) {
   constexpr int RS = D + kPad;
+  constexpr int RPW = kRB / NW;
   const int rows = uniform_clamp(r_end - r0, kRB);
   const u32x4 rs = rsrc_words32(src + (int64_t)r0 * H * D, (uint32_t)(rows * H * D * 2));
-  const int off = (wave * 8 * H + h) * D * 2 + lane * 16;
+  const int off = (wave * RPW * H + h) * D * 2 + lane * 16;
   if (lane < D / 8) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      // one add of a scalar row term (volatile: not hoisted into 8 registers)
+    for (int n = 0; n < RPW; ++n) {
+      // one add of a scalar row term (volatile: not hoisted into RPW registers)
       int voff;
       asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(n * H * D * 2), "v"(off));
-      lds_dma16(rs, base + (wave * 8 + n) * RS * 2, voff);
+      lds_dma16(rs, base + (wave * RPW + n) * RS * 2, voff);
     }
   }
 }
 
-template <typename T, int D, bool FQ>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
+template <typename T, int D, bool FQ, int NW>
+__global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
@@ -97,6 +100,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   constexpr int kDsplit = D >= 256 ? 2 : 1;
   constexpr int NDO = ND / kDsplit;  // 32-wide d tiles of dK/dV per workgroup
   static_assert(!FQ || kDsplit == 1, "the fused variant keeps all of d");
+  static_assert(!FQ || NW == 4, "the fused variant sums four waves' dQ rows");
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int dpart = kDsplit > 1 ? (int)(blockIdx.x % kDsplit) : 0;
@@ -112,13 +116,14 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   const bool wave_active = k0 + wave * 32 < k1;
 
   // stage query block qb: Q and dO rows by 16-byte DMA, LSE and delta (strided
-  // by H) by one 4-byte DMA per lane -- waves 0/2 LSE, 1/3 delta, so every
-  // wave issues the same count.  Rows past q1 arrive as zeros: Q = dO = 0
-  // there makes both of their products vanish whatever P is.
+  // by H) by one 4-byte DMA per lane -- even waves LSE, odd waves delta (the
+  // same bytes from every even or odd wave), so every wave issues the same
+  // count.  Rows past q1 arrive as zeros: Q = dO = 0 there makes both of
+  // their products vanish whatever P is.
   auto issue = [&](int qb, int buf) {
     unsigned char *base = smem_raw + buf * S::kBufBytes;
-    dma_rows<T, D>(q, qb, q1, H, h, lds_addr(base), wave, lane);
-    dma_rows<T, D>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
+    dma_rows<T, D, NW>(q, qb, q1, H, h, lds_addr(base), wave, lane);
+    dma_rows<T, D, NW>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
     const float *vec = (wave & 1) ? delta : lse;
     const int rows = uniform_clamp(q1 - qb, kRB);
     const u32x4 rv = rsrc_words32(vec + (int64_t)qb * H + h, (uint32_t)(rows * H * 4));
@@ -404,8 +409,8 @@ struct DqSmem {
   static constexpr int kBytes = 2 * kBuf * 2;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, float *delta,
     const T *__restrict__ o_fused, T *__restrict__ dq, float *__restrict__ part_dq,
@@ -427,20 +432,22 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   const bool row_ok = qrow < q1;
   const bool wave_active = q0 + wave * 32 < q1;
 
-  // key blocks staged through registers (waves 0-1 K, 2-3 V; rows past k1
-  // read as zero): a block's loads are issued before the previous block's
-  // compute and written to LDS after it.  (Per-row LDS-DMA moves only D*2
-  // bytes per instruction, which costs more than it saves here.)
-  const bool stage_k = wave < 2;
-  const int st = tid & 127;
+  // key blocks staged through registers (the first half of the waves K, the
+  // second V; rows past k1 read as zero): a block's loads are issued before
+  // the previous block's compute and written to LDS after it.  (Per-row
+  // LDS-DMA moves only D*2 bytes per instruction, which costs more than it
+  // saves here.)
+  constexpr int NS = 32 * NW;  // staging threads per tensor
+  const bool stage_k = wave < NW / 2;
+  const int st = tid & (NS - 1);
   const T *src = stage_k ? k : v;
-  Rows<D, 128> stg;
+  Rows<D, NS> stg;
   auto put = [&](int buf) {
     T *ks = smem + buf * S::kBuf;
-    store_rows<T, D, 128>(stg, stage_k ? ks : ks + S::kKs, RS, st);
+    store_rows<T, D, NS>(stg, stage_k ? ks : ks + S::kKs, RS, st);
   };
   const int nblk = (k1 - k0 + kRB - 1) / kRB;
-  if (nblk > 0) load_rows<T, D, 128>(stg, src, k0, k1, H, h, st);
+  if (nblk > 0) load_rows<T, D, NS>(stg, src, k0, k1, H, h, st);
 
   typename M::v8 qf[NC], dof[NC];
   // O rows for delta (fused mode), requested with Q and dO: one round trip
@@ -508,7 +515,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   // 48 VALU instructions per block).
   auto block = [&](int j, auto masked) {
     const int kb = k0 + j * kRB;
-    if (j + 1 < nblk) load_rows<T, D, 128>(stg, src, kb + kRB, k1, H, h, st);
+    if (j + 1 < nblk) load_rows<T, D, NS>(stg, src, kb + kRB, k1, H, h, st);
     if (wave_active) {
       const lds_cptr<T> ks = as_lds(smem + (j & 1) * S::kBuf);
       const lds_cptr<T> vs = ks + S::kKs;
@@ -599,43 +606,61 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 
 }  // namespace
 
+template <typename T, int D, int NW>
+void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
+  const int smem = DkvSmem<D>::kBytes;
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, false, NW>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false, NW>),
+                     dim3((unsigned)(a.n_kv * a.H * dsplit)), dim3(64 * NW), smem, st,
+                     (const T *)a.q, (const T *)a.k, (const T *)a.v, (const T *)a.dout,
+                     a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
+                     a.scale * kLog2e, a.scale, nullptr);
+}
+
+// The plan's key tile sets the workgroup: 32 keys per wave.
 template <typename T, int D>
 void launch_mfma_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
-  const int smem = DkvSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, false>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false>), dim3((unsigned)(a.n_kv * a.H * dsplit)),
-                     dim3(256),
-                     smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
-                     (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
-                     a.scale * kLog2e, a.scale, nullptr);
+  if constexpr (D == 128) {
+    if (a.k_tile == kVarlenWideTile) return launch_dkv_nw<T, D, 8>(a, st);
+  }
+  launch_dkv_nw<T, D, 4>(a, st);
 }
 
 template <typename T, int D>
 void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_fkv == 0) return;
   const int smem = FqSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, true>),
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, true, 4>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, true>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, true, 4>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
                      smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.fkv_items, a.H,
                      a.scale * kLog2e, a.scale, a.part_fq);
 }
 
-template <typename T, int D>
-void launch_mfma_varlen_dq(const VarlenArgs &a, hipStream_t st) {
-  if (a.n_items == 0) return;
+template <typename T, int D, int NW>
+void launch_dq_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = DqSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dq_kernel<T, D>),
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dq_kernel<T, D, NW>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_dq_kernel<T, D>), dim3((unsigned)(a.n_items * a.H)), dim3(256),
-                     smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
+  hipLaunchKernelGGL((varlen_dq_kernel<T, D, NW>), dim3((unsigned)(a.n_items * a.H)),
+                     dim3(64 * NW), smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta,
                      a.fuse_delta ? (const T *)a.o_in : nullptr, (T *)a.dq, a.part_o, a.items,
                      a.H, a.scale * kLog2e, a.scale);
+}
+
+// dQ runs over the forward's query tiles: 32 rows per wave.
+template <typename T, int D>
+void launch_mfma_varlen_dq(const VarlenArgs &a, hipStream_t st) {
+  if (a.n_items == 0) return;
+  if constexpr (D <= 128) {
+    if (a.q_tile == kVarlenWideTile) return launch_dq_nw<T, D, 8>(a, st);
+  }
+  launch_dq_nw<T, D, 4>(a, st);
 }
 
 #define VAFA_INST(T, D)                                                           \

@@ -1,11 +1,11 @@
 // Packed varlen FlashAttention on gfx950 matrix cores (bf16 / f16 inputs).
 //
 // Forward (replaces fa/kernels.py:64-175 and the split variant 516-628):
-// one workgroup = 4 waves = 128 query rows of one head; each wave owns 32
-// rows.  Key/value tiles of 64 keys are staged once per workgroup in LDS
-// (both row-major; V^T operands come from transposing LDS reads) with a
-// register prefetch of the next tile, so
-// each tile is read from HBM/L2 once for 128 queries.  Per 64-key tile a wave
+// one workgroup = NW waves (4 or 8, the plan's query tile / 32) of one head;
+// each wave owns 32 rows.  Key/value tiles of 64 keys are staged once per
+// workgroup in LDS (both row-major; V^T operands come from transposing LDS
+// reads) with a register prefetch of the next tile, so each tile is read
+// from HBM/L2 once for 128 or 256 queries.  Per 64-key tile a wave
 // issues 16 MFMAs for S^T = K Q^T and 16 for O^T += V^T P^T (D=128).  The
 // online softmax runs in the log2 domain against a lazily updated running
 // max: a tile's row max is taken (one cross-lane register swap, lane l <->
@@ -18,8 +18,7 @@ namespace vafa {
 
 namespace {
 
-constexpr int kBM = kVarlenQTile;  // 128 query rows per workgroup
-constexpr int kBN = 64;            // keys per LDS tile
+constexpr int kBN = 64;  // keys per LDS tile
 // LDS row padding (elements).  K is read by ds_read_b128 (rows as the A
 // operand) and V only by ds_read_b64_tr_b16 (V^T operands); measured on
 // gfx950 the two want different row strides: 16-byte row reads are
@@ -38,18 +37,21 @@ struct FwdSmem {
   static constexpr int kBytes = 2 * kBuf * 2;    // double buffered, 2 B/elt
 };
 
-// Global -> register stage of one K/V tile (zero-filled past k_end).
-template <int D>
+// Global -> register stage of one K/V tile over NT threads (zero-filled past
+// k_end; at D=32 with 512 threads half of them have no chunk).
+template <int D, int NT>
 struct TileRegs {
-  static constexpr int kKChunks = kBN * D / 8 / 256;  // 16 B chunks per thread
+  static constexpr int kTotal = kBN * D / 8;                // 16 B chunks per tensor
+  static constexpr int kKChunks = (kTotal + NT - 1) / NT;   // per thread
   u32x4 kc[kKChunks];
   u32x4 vc[kKChunks];
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void load_tile(TileRegs<D> &r, const T *__restrict__ k,
+template <typename T, int D, int NT>
+__device__ __forceinline__ void load_tile(TileRegs<D, NT> &r, const T *__restrict__ k,
                                           const T *__restrict__ v, int kbase, int k_end, int H,
                                           int h, int tid) {
+  using R = TileRegs<D, NT>;
   constexpr int CPR = D / 8;  // chunks per row
   // one buffer resource per tile: rows past k_end read as zero
   const int64_t row_bytes = (int64_t)H * D * 2;
@@ -57,28 +59,31 @@ __device__ __forceinline__ void load_tile(TileRegs<D> &r, const T *__restrict__ 
   const rsrc_t rk = make_rsrc(k + (int64_t)kbase * H * D, nbytes);
   const rsrc_t rv = make_rsrc(v + (int64_t)kbase * H * D, nbytes);
 #pragma unroll
-  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
-    const int ci = tid + 256 * i;
-    const int key = ci / CPR, dc = ci % CPR;
+  for (int i = 0; i < R::kKChunks; ++i) {
+    const int ci = tid + NT * i;
+    const int key = ci < R::kTotal ? ci / CPR : kBN, dc = ci % CPR;  // kBN: past the range
     r.kc[i] = buf_load16(rk, (key * H + h) * D * 2 + dc * 16);
   }
 #pragma unroll
-  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
-    const int ci = tid + 256 * i;
-    const int key = ci / CPR, dc = ci % CPR;
+  for (int i = 0; i < R::kKChunks; ++i) {
+    const int ci = tid + NT * i;
+    const int key = ci < R::kTotal ? ci / CPR : kBN, dc = ci % CPR;
     r.vc[i] = buf_load16(rv, (key * H + h) * D * 2 + dc * 16);
   }
 }
 
-template <typename T, int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D> &r, T *ks, T *vs, int tid) {
+template <typename T, int D, int NT>
+__device__ __forceinline__ void store_tile(const TileRegs<D, NT> &r, T *ks, T *vs, int tid) {
+  using R = TileRegs<D, NT>;
   constexpr int CPR = D / 8;
 #pragma unroll
-  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
-    const int ci = tid + 256 * i;
-    const int key = ci / CPR, dc = ci % CPR;
-    *reinterpret_cast<u32x4 *>(ks + key * FwdSmem<D>::KSK + dc * 8) = r.kc[i];
-    *reinterpret_cast<u32x4 *>(vs + key * FwdSmem<D>::KSV + dc * 8) = r.vc[i];
+  for (int i = 0; i < R::kKChunks; ++i) {
+    const int ci = tid + NT * i;
+    if (R::kTotal % NT == 0 || ci < R::kTotal) {
+      const int key = ci / CPR, dc = ci % CPR;
+      *reinterpret_cast<u32x4 *>(ks + key * FwdSmem<D>::KSK + dc * 8) = r.kc[i];
+      *reinterpret_cast<u32x4 *>(vs + key * FwdSmem<D>::KSV + dc * 8) = r.vc[i];
+    }
   }
 }
 
@@ -210,8 +215,9 @@ __device__ __forceinline__ void fwd_tile(const T *ks, const T *vs,
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
+// two waves per SIMD (one at D=256, whose registers take the whole file)
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     T *__restrict__ o, float *__restrict__ lse, float *__restrict__ part_o,
     float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, float c) {
@@ -254,23 +260,24 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   float m_run = -kHuge, l_part = 0.f;
 
+  constexpr int NT = 64 * NW;
   const int nt = (k1 - k0 + kBN - 1) / kBN;
-  TileRegs<D> regs;
+  TileRegs<D, NT> regs;
   if (nt > 0) {
-    load_tile<T, D>(regs, k, v, k0, k1, H, h, tid);
-    store_tile<T, D>(regs, smem, smem + FwdSmem<D>::kKs, tid);
+    load_tile<T, D, NT>(regs, k, v, k0, k1, H, h, tid);
+    store_tile<T, D, NT>(regs, smem, smem + FwdSmem<D>::kKs, tid);
   }
   __syncthreads();
 
   for (int j = 0; j < nt; ++j) {
     const int kbase = k0 + j * kBN;
-    if (j + 1 < nt) load_tile<T, D>(regs, k, v, kbase + kBN, k1, H, h, tid);
+    if (j + 1 < nt) load_tile<T, D, NT>(regs, k, v, kbase + kBN, k1, H, h, tid);
     const T *ks = smem + (j & 1) * FwdSmem<D>::kBuf;
     const T *vs = ks + FwdSmem<D>::kKs;
     if (wave_active) fwd_tile<T, D>(ks, vs, qf, acc, m_run, l_part, c, kbase, k1, lane);
     if (j + 1 < nt) {
       T *nks = smem + ((j + 1) & 1) * FwdSmem<D>::kBuf;
-      store_tile<T, D>(regs, nks, nks + FwdSmem<D>::kKs, tid);
+      store_tile<T, D, NT>(regs, nks, nks + FwdSmem<D>::kKs, tid);
     }
     __syncthreads();
   }
@@ -310,15 +317,24 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
 
 }  // namespace
 
+template <typename T, int D, int NW>
+void launch_fwd_nw(const VarlenArgs &a, hipStream_t st) {
+  const int smem = FwdSmem<D>::kBytes;
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D, NW>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  hipLaunchKernelGGL((varlen_fwd_kernel<T, D, NW>), dim3((unsigned)(a.n_items * a.H)),
+                     dim3(64 * NW), smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
+                     (T *)a.o, a.lse, a.part_o, a.part_lse, a.items, a.H, a.scale * kLog2e);
+}
+
+// The plan's query tile sets the workgroup: 32 rows per wave.
 template <typename T, int D>
 void launch_mfma_varlen_fwd(const VarlenArgs &a, hipStream_t st) {
   if (a.n_items == 0) return;
-  const int smem = FwdSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_fwd_kernel<T, D>), dim3((unsigned)(a.n_items * a.H)), dim3(256),
-                     smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v, (T *)a.o, a.lse,
-                     a.part_o, a.part_lse, a.items, a.H, a.scale * kLog2e);
+  if constexpr (D <= 128) {
+    if (a.q_tile == kVarlenWideTile) return launch_fwd_nw<T, D, 8>(a, st);
+  }
+  launch_fwd_nw<T, D, 4>(a, st);
 }
 
 #define VAFA_INST(T, D) template void launch_mfma_varlen_fwd<T, D>(const VarlenArgs &, hipStream_t);

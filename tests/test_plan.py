@@ -198,14 +198,16 @@ def check_varlen_plan(q_lens, k_lens, H=4, D=64):
     assert dq.tolist() == [r for r in fwd.tolist() if not fused[r[5]]]
     assert dqc.tolist() == [r for r in comb.tolist() if not fused[r[4]]]
     assert p.info.max_dqc_rows == max([r[1] - r[0] for r in dqc.tolist()], default=0)
-    # 6) fused partial rows: tile j of a segment writes rows pbase + j*Lq + r,
-    #    the tiles of all fused segments tile [0, n_fpart_rows) exactly once
+    # 6) fused partial rows: chunk j of a segment writes rows pbase + j*Lq + r,
+    #    the chunks of all fused segments tile [0, n_fpart_rows) exactly once
     assert sorted(r[4] for r in fcomb.tolist()) == [s for s in range(len(q_lens))
                                                      if fused[s] and k_lens[s] > 0]
     fused_used = np.zeros(p.info.n_fpart_rows, dtype=np.int64)
     tiles = {}
+    CH = 3 * 128  # a fused item walks a chunk of three 128-key tiles
     for k0, k1, q0, q1, seg, pbase, j, nt in fkv.tolist():
-        assert k0 == ck[seg] + 128 * j and nt == -(-int(k_lens[seg]) // 128)
+        assert k0 == ck[seg] + CH * j and nt == -(-int(k_lens[seg]) // CH)
+        assert k1 == min(k0 + CH, ck[seg + 1])
         tiles.setdefault(seg, []).append((j, pbase))
     for q0, q1, pbase, nt, seg, *_ in fcomb.tolist():
         R = q1 - q0

@@ -111,6 +111,17 @@ __device__ __forceinline__ u32x4 rsrc_words32(const void *base, uint32_t bytes) 
   return r;
 }
 
+// A wave-uniform pointer computed on the vector unit (a 64-bit multiply,
+// which the scalar unit lacks), moved back to scalar registers so that the
+// buffer descriptors built from it stay scalar.
+template <typename P>
+__device__ __forceinline__ P *uniform_ptr(P *p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  return reinterpret_cast<P *>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
+
 // min(max(n, 0), hi), made wave-uniform: a clamp compiles to v_med3_i32,
 // which would drag the byte counts formed from it (and their 64-bit
 // multiplies) onto the vector unit.

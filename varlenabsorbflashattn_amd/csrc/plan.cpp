@@ -291,12 +291,12 @@ int vafa_chunk_indices(const int64_t *cu, int64_t n1, int32_t BT, int32_t *out, 
 //                   (same order, same partial rows): the dQ pass, which reuses
 //                   the forward's split layout with its own partial buffer.
 //   fkv section   : fused segments (at most kFusedMaxQ queries, D <=
-//                   kFusedMaxD), one item per key tile:
-//                   {k0, k1, q0, q1, seg, pbase, tile, ntiles}; the tile's
-//                   scaled fp32 dQ partial of query q lands in row
+//                   kFusedMaxD), one item per chunk of kFusedTiles 128-key
+//                   tiles: {k0, k1, q0, q1, seg, pbase, chunk, nchunks}; the
+//                   chunk's scaled fp32 dQ partial of query q lands in row
 //                   pbase + (q - q0).
-//   fcomb section : one item per fused segment, {q0, q1, pbase, ntiles, seg,
-//                   0, 0, 0}: tile t of the segment owns rows
+//   fcomb section : one item per fused segment, {q0, q1, pbase, nchunks, seg,
+//                   0, 0, 0}: chunk t of the segment owns rows
 //                   pbase + t*(q1-q0) + r (the comb layout), summed in order.
 int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H, int64_t D,
                      int32_t *plan, int64_t plan_cap, vafa_plan_info *info) {
@@ -344,8 +344,8 @@ int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64
       }
       prow += ns * rows;
     }
-    // fused segments (D <= 64, so BK is kVarlenTile there too) keep 128-key tiles
-    const int64_t bk = fused[s] ? kVarlenTile : BK;
+    // fused segments walk chunks of kFusedTiles 128-key tiles
+    const int64_t bk = fused[s] ? (int64_t)kFusedTiles * kVarlenTile : BK;
     const int64_t ntiles = (lk + bk - 1) / bk;
     for (int64_t k = k0, j = 0; k < k1; k += bk, ++j) {
       const int64_t ke = std::min(k + bk, k1);

@@ -40,12 +40,13 @@ constexpr SplitPolicy kAbsorbPolicy{0, 1 << 30, 1024, 1, 16, 1024, 1024, 64, 32}
 constexpr int64_t kAbsorbSlots = 768;
 constexpr int64_t kAbsorbSplitSlack = 3;
 
-// Varlen backward, fused K-major path (dQ, dK, dV in one kernel per 128-key
-// tile, fp32 dQ partials per tile summed in order): segments with at most
-// kFusedMaxQ queries and at least kFusedMinK keys, at head dims up to
-// kFusedMaxD.  Each tile writes Lq*D*4 bytes of partial dQ (plus the read back
-// in the sum) and saves the second read of its K/V rows that the query-major
-// dQ kernel makes.  Measured on the MI355X (64 segments x 8192 keys, backward
+// Varlen backward, fused K-major path (dQ, dK, dV in one kernel, fp32 dQ
+// partials per key chunk summed in order): segments with at most kFusedMaxQ
+// queries and at least kFusedMinK keys, at head dims up to kFusedMaxD.  Each
+// chunk writes Lq*D*4 bytes of partial dQ (plus the read back in the sum) and
+// saves the second read of its K/V rows that the query-major dQ kernel makes.
+// Measured on the MI355X with one 128-key tile per item (64 segments x 8192
+// keys, backward
 // ms, two-kernel vs fused): H=4 D=64 Lq=1/8/16: 0.447/0.440/0.451 vs
 // 0.379/0.387/0.394; Lq=32 0.443 vs 0.440; Lq=48/64 0.487/0.472 vs
 // 0.519/0.561.  At D=128 the fused kernel holds one workgroup per CU (256
@@ -54,6 +55,13 @@ constexpr int64_t kAbsorbSplitSlack = 3;
 constexpr int kFusedMaxQ = 16;
 constexpr int kFusedMinK = 1;
 constexpr int kFusedMaxD = 64;
+// A fused item walks up to kFusedTiles 128-key tiles of one segment (the
+// query block staged once, dQ summed over the chunk in registers).  Measured
+// on the MI355X, backward ms for 1 / 2 / 3 / 4 tiles per item: 64 x 16 queries
+// x 8192 keys (H=4, D=64) 0.667 / 0.666 / 0.607 / 0.750; 256 x 8 x 2048 keys
+// 0.644 / 0.663 / 0.638 / 0.780; 32 x 1 x 32768 keys (H=8) 2.47 / 2.41 /
+// 2.37 / 2.44.
+constexpr int kFusedTiles = 3;
 
 // Workgroups are dispatched round-robin over this many XCDs (one L2 each):
 // workgroup i runs on XCD i % kXcds.

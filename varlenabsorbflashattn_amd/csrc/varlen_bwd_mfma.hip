@@ -1,6 +1,6 @@
 // Packed varlen FlashAttention backward on gfx950 matrix cores.
 //
-// Two deterministic kernels (no atomics), both recomputing P = exp2(S*c - LSE)
+// Deterministic kernels (no atomics), all recomputing P = exp2(S*c - LSE)
 // from the forward's log2-domain LSE (fa/kernels.py:233-494):
 //   * dK/dV, key-major: a workgroup owns the plan's key tile (128 or 256 keys)
 //     of one head (32 per wave, K and V held in registers as MFMA operands)
@@ -12,12 +12,11 @@
 //       dV^T += dO^T P,  dK^T += Q^T dS           (4 products per block)
 //   * dQ, query-major over the forward's plan items (including split-K
 //     partials): S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
-//   * fused dQ/dK/dV, key-major (segments with few queries): the dK/dV kernel
-//     with FQ = true also forms dQ^T = K^T dS^T for its 128 keys per query
-//     block (dS^T through LDS, K^T operands read once, transposed, from the
-//     wave's K rows), sums the four waves' contributions in a fixed order and
-//     writes scaled fp32 partial rows, one set per key tile, that an ordered
-//     sum turns into dQ (the dead template of fa/kernels.py:923-1099).
+//   * fused dQ/dK/dV, key-major (segments with one query block): a workgroup
+//     walks a chunk of 128-key tiles with the query block staged once, forms
+//     dK/dV per tile and dQ^T = K^T dS^T over the whole chunk, and writes one
+//     set of scaled fp32 partial dQ rows per chunk, which an ordered sum turns
+//     into dQ (the dead template of fa/kernels.py:923-1099).
 // The dQ kernel stages K / V blocks through registers.  Its row statistics stay
 // per lane (lane <-> query row); the dK/dV kernel reads LSE and delta of its
 // 32-row block from LDS.  LDS operands are read a few products ahead of the
@@ -44,22 +43,6 @@ struct DkvSmem {
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
-// Extra LDS of the fused variant, after DkvSmem: region R holds first the
-// waves' K rows (staged once for the transposed K^T reads) and then, per query
-// block, the four waves' dQ^T contributions [wave][q][D + 4] fp32; then one
-// [32 keys][40] dS^T tile per wave.
-template <int D>
-struct FqSmem {
-  static constexpr int kKtBytes = 4 * 32 * DkvSmem<D>::RS * 2;
-  static constexpr int kRS = D + 4;
-  static constexpr int kRedBytes = 4 * 32 * kRS * 4;
-  static constexpr int kROff = DkvSmem<D>::kBytes;
-  static constexpr int kRBytes = kKtBytes > kRedBytes ? kKtBytes : kRedBytes;
-  static constexpr int kDsS = 40;
-  static constexpr int kDsOff = kROff + kRBytes;
-  static constexpr int kBytes = kDsOff + 4 * 32 * kDsS * 2;
-};
-
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
 // past r_end read as zero) into a padded [32][RS] block: wave w of NW moves
 // rows RPW*w .. RPW*w + RPW-1 (RPW = 32/NW), one instruction per row with
@@ -84,12 +67,12 @@ __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H,
   }
 }
 
-template <typename T, int D, bool FQ, int NW>
+template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
-    float scale, float *__restrict__ part_dq) {
+    float scale) {
   using M = Mfma<T>;
   using S = DkvSmem<D>;
   constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
@@ -99,8 +82,6 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   // not fit beside the K/V operands and spilled.
   constexpr int kDsplit = D >= 256 ? 2 : 1;
   constexpr int NDO = ND / kDsplit;  // 32-wide d tiles of dK/dV per workgroup
-  static_assert(!FQ || kDsplit == 1, "the fused variant keeps all of d");
-  static_assert(!FQ || NW == 4, "the fused variant sums four waves' dQ rows");
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int dpart = kDsplit > 1 ? (int)(blockIdx.x % kDsplit) : 0;
@@ -147,22 +128,6 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       vf[cc] = as_v8<T>(b);
     }
   }
-  // fused: the A operands of dQ^T = K^T dS^T (loop-invariant), read
-  // transposed from the wave's own K rows staged in LDS region R
-  typename M::v8 ktf[FQ ? 2 * ND : 1];
-  if constexpr (FQ) {
-    if (wave_active) {
-      T *kt = reinterpret_cast<T *>(smem_raw + FqSmem<D>::kROff) + wave * 32 * RS;
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc)
-        *reinterpret_cast<typename M::v8 *>(kt + lrow * RS + cc * 16 + lhalf * 8) = kf[cc];
-#pragma unroll
-      for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) ktf[hk * ND + dt] = tr_operand<T>(kt, RS, 16 * hk, 32 * dt, lane);
-    }
-  }
-  const int pbase = FQ ? it.v[5] : 0;
   f32x16 adk[NDO], adv[NDO];
 #pragma unroll
   for (int i = 0; i < NDO; ++i)
@@ -281,68 +246,6 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if constexpr (FQ) {
-        // dS of this lane (key lrow; queries 8*(r/4) + 4*lhalf + r%4) to LDS
-        // as dS^T [key][query], rounded to T as for dK
-        T *dst = reinterpret_cast<T *>(smem_raw + FqSmem<D>::kDsOff) + wave * 32 * FqSmem<D>::kDsS;
-        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          T4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(dp[4 * r4 + e]);
-          *reinterpret_cast<T4 *>(dst + lrow * FqSmem<D>::kDsS + 8 * r4 + 4 * lhalf) = w;
-        }
-        // dQ^T (D x 32 queries) = K^T dS^T over the wave's 32 keys; the
-        // dS^T operand is read transposed in the key order of the K^T reads
-        f32x16 dqa[ND];
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dqa[dt][r] = 0.f;
-#pragma unroll
-        for (int hk = 0; hk < 2; ++hk) {
-          const typename M::v8 b = tr_operand<T>(dst, FqSmem<D>::kDsS, 16 * hk, 0, lane);
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt) dqa[dt] = M::mma(ktf[hk * ND + dt], b, dqa[dt]);
-        }
-        // this wave's rows [query][d] of the reduction region
-        float *red = reinterpret_cast<float *>(smem_raw + FqSmem<D>::kROff) +
-                     wave * 32 * FqSmem<D>::kRS;
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            f32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = dqa[dt][4 * r4 + e];
-            *reinterpret_cast<f32x4 *>(red + lrow * FqSmem<D>::kRS + 32 * dt + 8 * r4 +
-                                       4 * lhalf) = w;
-          }
-      }
-    }
-    if constexpr (FQ) {
-      // ordered sum of the active waves' dQ^T rows, scaled: this key tile's
-      // partial dQ rows of the block's queries (the next iteration's barrier
-      // orders these reads before the region is written again)
-      __syncthreads();
-      const int nact = (k1 - k0 + 31) / 32 < 4 ? (k1 - k0 + 31) / 32 : 4;
-      const int row = tid >> 3, cs = tid & 7;  // 32 rows x 8 column segments
-      const int qb = q0 + j * kRB;
-      if (qb + row < q1) {
-        const float *red = reinterpret_cast<const float *>(smem_raw + FqSmem<D>::kROff);
-        float *prow = part_dq + ((int64_t)(pbase + qb - q0 + row) * H + h) * D;
-#pragma unroll
-        for (int c4 = 0; c4 < D / 32; ++c4) {
-          const int col = cs * (D / 8) + 4 * c4;
-          f32x4 acc = *reinterpret_cast<const f32x4 *>(red + row * FqSmem<D>::kRS + col);
-          for (int w = 1; w < nact; ++w)
-            acc += *reinterpret_cast<const f32x4 *>(red + (w * 32 + row) * FqSmem<D>::kRS + col);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[e] *= scale;
-          *reinterpret_cast<f32x4 *>(prow + col) = acc;
-        }
-      }
     }
   }
   wait_vmcnt<0>();
@@ -365,6 +268,266 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       *reinterpret_cast<T4 *>(dkr + d) = wk;
       *reinterpret_cast<T4 *>(dvr + d) = wv;
     }
+}
+
+// Fused K-major dQ/dK/dV for segments with at most kFusedMaxQ (<= 32)
+// queries at D <= 64 (the dead template of fa/kernels.py:923-1099, planner
+// fa/chunk_indices.py:290-460).  A workgroup owns one (segment, head) and a
+// chunk of up to kFusedTiles 128-key tiles; the segment's single query block
+// (Q, dO, LSE, delta) is staged once.  Per tile each wave holds its 32 keys'
+// K / V rows as operands -- the next tile's are requested into the same
+// registers once S and dP are formed -- forms S = Q K^T, dP = dO V^T, P and
+// dS, accumulates
+// dV^T += dO^T P and dK^T += Q^T dS (stored at the end of the tile) and
+// dQ^T += K^T dS^T over all of its tiles in registers (dS rounded to T as
+// for dK; K^T and dS^T operands read transposed from the wave's own LDS rows).
+// At the end the four waves' dQ^T are summed in a fixed order through LDS and
+// written, scaled, as the chunk's fp32 partial rows pbase + r, which
+// sum_combine_kernel adds in chunk order.
+template <int D>
+struct FusedSmem {
+  static constexpr int RS = D + kPad;
+  static constexpr int kQOff = 0;                     // Q block [32][RS]
+  static constexpr int kDoOff = kRB * RS * 2;         // dO block [32][RS]
+  static constexpr int kLsOff = 2 * kRB * RS * 2;     // LSE [32], delta [32]
+  static constexpr int kROff = kLsOff + 2 * kRB * 4;  // K rows, later the dQ^T sums
+  static constexpr int kRS = D + 4;                   // fp32 row stride of the sums
+  static constexpr int kKtBytes = 4 * 32 * RS * 2;
+  static constexpr int kRedBytes = 4 * 32 * kRS * 4;
+  static constexpr int kDsS = 40;                     // dS^T [32 keys][40]
+  static constexpr int kDsOff = kROff + (kKtBytes > kRedBytes ? kKtBytes : kRedBytes);
+  static constexpr int kBytes = kDsOff + 4 * 32 * kDsS * 2;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
+    const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
+    const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
+    T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
+    float scale, float *__restrict__ part_dq) {
+  using M = Mfma<T>;
+  using S = FusedSmem<D>;
+  using v8 = typename M::v8;
+  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  constexpr int kPre = 4;
+  static_assert(D <= 64, "the fused kernel serves D <= 64");
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int k0 = it.v[0], k1 = it.v[1], q0 = it.v[2], q1 = it.v[3], pbase = it.v[5];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int lrow = lane & 31, lhalf = lane >> 5;
+
+  // the query block (rows past q1 arrive as zeros: Q = dO = 0 there makes
+  // all of their products vanish whatever P is); even waves DMA LSE, odd
+  // waves delta
+  dma_rows<T, D, 4>(q, q0, q1, H, h, lds_addr(smem_raw + S::kQOff), wave, lane);
+  dma_rows<T, D, 4>(dout, q0, q1, H, h, lds_addr(smem_raw + S::kDoOff), wave, lane);
+  {
+    const float *vec = (wave & 1) ? delta : lse;
+    const int rows = uniform_clamp(q1 - q0, kRB);
+    const u32x4 rv = rsrc_words32(vec + (int64_t)q0 * H + h, (uint32_t)(rows * H * 4));
+    if (lane < kRB)
+      lds_dma4(rv, lds_addr(smem_raw + S::kLsOff + (wave & 1) * kRB * 4), lane * H * 4);
+  }
+
+  // K / V operands of tile t: this wave's 32 keys (keys past k1 read as zero;
+  // their P needs no masking: zero K and V rows make their dQ contribution
+  // vanish, and their dK / dV rows are never stored)
+  // (a chunk holds at most kFusedTiles * 128 keys: its byte count is formed
+  // on the scalar unit in 32 bits, which keeps the descriptors in SGPRs)
+  const uint32_t kv_bytes = (uint32_t)(k1 - k0) * (uint32_t)(H * D * 2);
+  const rsrc_t rk = make_rsrc32(uniform_ptr(k + (int64_t)k0 * H * D), kv_bytes);
+  const rsrc_t rvv = make_rsrc32(uniform_ptr(v + (int64_t)k0 * H * D), kv_bytes);
+  const int koff = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
+  auto load_kv = [&](int t, v8 (&kk)[NC], v8 (&vv)[NC]) {
+    const int off = koff + t * 128 * H * D * 2;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      kk[cc] = as_v8<T>(buf_load16(rk, off + cc * 32));
+      vv[cc] = as_v8<T>(buf_load16(rvv, off + cc * 32));
+    }
+  };
+  v8 kf[NC], vf[NC];
+  load_kv(0, kf, vf);
+
+  f32x16 dqa[ND];  // dQ^T [d][query] over all of the chunk's keys
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dqa[dt][r] = 0.f;
+
+  const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(smem_raw + S::kQOff));
+  const lds_cptr<T> ds_ = as_lds(reinterpret_cast<const T *>(smem_raw + S::kDoOff));
+  const float *ls = reinterpret_cast<const float *>(smem_raw + S::kLsOff);
+  T *kt = reinterpret_cast<T *>(smem_raw + S::kROff) + wave * 32 * RS;
+  T *dst = reinterpret_cast<T *>(smem_raw + S::kDsOff) + wave * 32 * S::kDsS;
+  const int a_off = lrow * RS + lhalf * 8;
+  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+                    4 * (lane & 3);
+  const int ntile = (k1 - k0 + 127) / 128;
+  wait_vmcnt<0>();
+  __syncthreads();  // the query block is visible
+
+  // one tile; false when this wave has no keys in it (nor in later tiles)
+  auto tile = [&](int t) -> bool {
+    const int key = k0 + t * 128 + wave * 32 + lrow;
+    if (k0 + t * 128 + wave * 32 >= k1) return false;
+    // K rows to this wave's LDS rows, K^T operands of dQ^T read back
+    // transposed (LDS operations of one wave execute in order)
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+      *reinterpret_cast<v8 *>(kt + lrow * RS + cc * 16 + lhalf * 8) = kf[cc];
+    v8 ktf[2 * ND];
+#pragma unroll
+    for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) ktf[hk * ND + dt] = tr_operand<T>(kt, RS, 16 * hk, 32 * dt, lane);
+    // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
+    auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+    u32x4 ring[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 2 * NC; ++i) {
+      const v8 a = as_v8<T>(ring[i % kPre]);
+      if (i & 1)
+        dp = M::mma(a, vf[i >> 1], dp);
+      else
+        s = M::mma(a, kf[i >> 1], s);
+      if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // K / V of the next tile, in flight under the rest of this one
+    if (t + 1 < ntile) load_kv(t + 1, kf, vf);
+    // P = exp2(S*c - LSE), dS = P (dP - delta); row r of a lane is query
+    // 8*(r/4) + 4*lhalf + r%4 of the block
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
+      const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = g * 4 + e;
+        const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
+        s[r] = p;
+        dp[r] = p * (dp[r] - Dl[e]);
+      }
+    }
+    v8 pb[2], sb[2];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      pb[mm] = pack8<T>(s, 8 * mm);
+      sb[mm] = pack8<T>(dp, 8 * mm);
+    }
+    // dS^T [key][query] of this wave, rounded to T as for dK
+    typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      T4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(dp[4 * r4 + e]);
+      *reinterpret_cast<T4 *>(dst + lrow * S::kDsS + 8 * r4 + 4 * lhalf) = w;
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS: operand i -> d tile i % ND, query
+    // half (i / ND) >> 1, dO^T when (i / ND) is even, else Q^T
+    f32x16 adk[ND], adv[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) adk[i][r] = adv[i][r] = 0.f;
+    auto top = [&](int i) {
+      const lds_cptr<T> p =
+          (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
+      return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+    };
+    v8 tring[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4 * ND; ++i) {
+      const int dt = i % ND, q2 = i / ND, mm = q2 >> 1;
+      if (q2 & 1)
+        adk[dt] = M::mma(tring[i % kPre], sb[mm], adk[dt]);
+      else
+        adv[dt] = M::mma(tring[i % kPre], pb[mm], adv[dt]);
+      if (i + kPre < 4 * ND) tring[i % kPre] = top(i + kPre);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // dQ^T += K^T dS^T over the wave's 32 keys (dS^T read transposed in the
+    // key order of the K^T operands)
+#pragma unroll
+    for (int hk = 0; hk < 2; ++hk) {
+      const v8 b = tr_operand<T>(dst, S::kDsS, 16 * hk, 0, lane);
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) dqa[dt] = M::mma(ktf[hk * ND + dt], b, dqa[dt]);
+    }
+    if (key < k1) {
+      T *dkr = dk + ((int64_t)key * H + h) * D;
+      T *dvr = dv + ((int64_t)key * H + h) * D;
+#pragma unroll
+      for (int dtile = 0; dtile < ND; ++dtile)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          T4 wk, wv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wk[e] = static_cast<T>(adk[dtile][g * 4 + e] * scale);
+            wv[e] = static_cast<T>(adv[dtile][g * 4 + e]);
+          }
+          const int d = dtile * 32 + g * 8 + lhalf * 4;
+          *reinterpret_cast<T4 *>(dkr + d) = wk;
+          *reinterpret_cast<T4 *>(dvr + d) = wv;
+        }
+    }
+    return true;
+  };
+  // tile 0 peeled: every entry to the loop then comes after a tile whose
+  // dK / dV stores follow its K / V requests, so the compiler's wait for the
+  // K / V operands at the top of a tile leaves those stores in flight
+  if (ntile > 0 && tile(0))
+    for (int t = 1; t < ntile; ++t)
+      if (!tile(t)) break;
+
+  // ordered sum of the four waves' dQ^T (a wave without keys adds zeros),
+  // scaled: the chunk's partial dQ rows
+  __syncthreads();  // every wave is done with its K rows (region R is reused)
+  {
+    float *red = reinterpret_cast<float *>(smem_raw + S::kROff) + wave * 32 * S::kRS;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        f32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = dqa[dt][4 * r4 + e];
+        *reinterpret_cast<f32x4 *>(red + lrow * S::kRS + 32 * dt + 8 * r4 + 4 * lhalf) = w;
+      }
+  }
+  __syncthreads();
+  const int row = tid >> 3, cs = tid & 7;  // 32 rows x 8 column segments
+  if (q0 + row < q1) {
+    const float *red = reinterpret_cast<const float *>(smem_raw + S::kROff);
+    float *prow = part_dq + ((int64_t)(pbase + row) * H + h) * D;
+#pragma unroll
+    for (int c4 = 0; c4 < D / 32; ++c4) {
+      const int col = cs * (D / 8) + 4 * c4;
+      f32x4 acc = *reinterpret_cast<const f32x4 *>(red + row * S::kRS + col);
+#pragma unroll
+      for (int w = 1; w < 4; ++w)
+        acc += *reinterpret_cast<const f32x4 *>(red + (w * 32 + row) * S::kRS + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] *= scale;
+      *reinterpret_cast<f32x4 *>(prow + col) = acc;
+    }
+  }
 }
 
 // A [kRB x D] block of a [T, H, D] tensor staged through registers: 16-byte
@@ -609,14 +772,14 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 template <typename T, int D, int NW>
 void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = DkvSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, false, NW>),
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, NW>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, false, NW>),
+  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, NW>),
                      dim3((unsigned)(a.n_kv * a.H * dsplit)), dim3(64 * NW), smem, st,
                      (const T *)a.q, (const T *)a.k, (const T *)a.v, (const T *)a.dout,
                      a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
-                     a.scale * kLog2e, a.scale, nullptr);
+                     a.scale * kLog2e, a.scale);
 }
 
 // The plan's key tile sets the workgroup: 32 keys per wave.
@@ -632,10 +795,10 @@ void launch_mfma_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
 template <typename T, int D>
 void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_fkv == 0) return;
-  const int smem = FqSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, true, 4>),
+  const int smem = FusedSmem<D>::kBytes;
+  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fkv_kernel<T, D>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_dkv_kernel<T, D, true, 4>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
+  hipLaunchKernelGGL((varlen_fkv_kernel<T, D>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
                      smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.fkv_items, a.H,
                      a.scale * kLog2e, a.scale, a.part_fq);

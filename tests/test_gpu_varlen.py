@@ -25,6 +25,9 @@ CASES = [
     ("block_aligned", [256, 256], [128, 128], 64),
     ("head_dim_128", [200, 300], [150, 250], 128),
     ("head_dim_32", [70, 5], [90, 200], 32),
+    # long segments hold most of the work: 256-row query tiles (8-wave forward / dQ)
+    ("head_dim_32_wide", [300, 140, 9], [200, 260, 50], 32),
+    ("head_dim_16_wide", [260, 20], [300, 3000], 16),
     ("head_dim_256", [130, 3], [77, 300], 256),
     # D=256 dK/dV runs as two workgroups per key tile (one half of d each):
     # several key tiles, a key tail and a split-K forward

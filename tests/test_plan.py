@@ -425,3 +425,21 @@ def test_config_plans():
     for cfg in (W.config4(seed=0), W.config5(seed=0)):
         p = _lib.plan_absorb(_cu(cfg.q_lens), _cu(cfg.k_lens), cfg.H, cfg.D_in, cfg.D_H)
         assert p.info.n_comb == 0 and p.info.max_split == 1, cfg.name
+
+
+def test_varlen_entry_rejects_plan_of_another_head_dim():
+    """A plan with 256-key dK/dV tiles (built for D=128) does not fit the D=64
+    kernels: the C ABI refuses it before touching any device memory."""
+    import ctypes as C
+    cq, ck = _cu([200, 300]), _cu([150, 250])
+    p = _lib.plan_varlen(cq, ck, 2, 128)
+    assert (p.info.q_tile, p.info.k_tile) == (256, 256)
+    lib = _lib.lib()
+    rc = lib.vafa_varlen_bwd(None, None, None, None, None, None, None, None, None, None,
+                             C.byref(p.info), 64, _lib.DT_BF16, 0.125, None, 0, None)
+    assert rc != 0 and "head_dim 64" in _lib.last_error()
+    rc = lib.vafa_varlen_fwd(None, None, None, None, None, None, C.byref(p.info), 256,
+                             _lib.DT_BF16, 0.0625, None, 0, None)
+    assert rc != 0 and "head_dim 256" in _lib.last_error()
+    with pytest.raises(ValueError, match="build the plan with this head_dim"):
+        _lib.check(rc)

@@ -101,7 +101,11 @@ typedef struct vafa_plan_info {
   int64_t off_qt, n_qt;           /* unsplit query tiles (absorb dU pass)  */
   int64_t n_part_rows;            /* partial rows written by split items   */
   int64_t plan_ints;              /* total plan length in int32            */
-  int64_t q_tile, k_tile;         /* tile sizes the plan was built for     */
+  int64_t q_tile, k_tile;         /* tile sizes the plan was built for:
+                                     varlen picks 128 or 256 per call (256
+                                     only for the head dims whose kernels run
+                                     it; entry points called with another D
+                                     return VAFA_ERR_VALUE)                  */
   int64_t max_split;              /* largest number of splits of one tile  */
   int64_t max_comb_rows;          /* most rows (tokens) of one combine item */
   int64_t n_kv_res;               /* absorb: the leading key-tile items whose
@@ -113,15 +117,16 @@ typedef struct vafa_plan_info {
   int64_t off_dq, n_dq;           /* dQ-pass items                          */
   int64_t off_dqc, n_dqc;         /* dQ-pass combine items                  */
   int64_t max_dqc_rows;
-  int64_t off_fkv, n_fkv;         /* fused key-tile items                   */
+  int64_t off_fkv, n_fkv;         /* fused key-chunk items                  */
   int64_t off_fcomb, n_fcomb;     /* fused dQ-partial sums                  */
   int64_t n_fpart_rows;           /* fused dQ partial rows                  */
   int64_t max_fcomb_rows;
 } vafa_plan_info;
 
 /* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).
- * cu_q/cu_k: host int64 [n1].  D selects tile sizes.  Call with plan==NULL
- * to size (info->plan_ints), then with a buffer of that many int32. */
+ * cu_q/cu_k: host int64 [n1].  D and the segment lengths select the tile
+ * sizes: the plan serves calls with this head dim.  Call with plan==NULL to
+ * size (info->plan_ints), then with a buffer of that many int32. */
 VAFA_API int vafa_plan_varlen(const int64_t *cu_q, const int64_t *cu_k, int64_t n1, int64_t H,
                      int64_t D, int32_t *plan, int64_t plan_cap, vafa_plan_info *info);
 

@@ -121,6 +121,12 @@ typedef struct vafa_plan_info {
   int64_t off_fcomb, n_fcomb;     /* fused dQ-partial sums                  */
   int64_t n_fpart_rows;           /* fused dQ partial rows                  */
   int64_t max_fcomb_rows;
+  /* varlen forward grid: 1 = the H heads of a forward item run on one XCD
+   * (most of the work lies in segments of at most 128 queries, whose items
+   * share no key range: the heads then read whole token rows together);
+   * 0 = item-major with heads innermost (the query tiles of a segment share
+   * its K/V in one XCD's L2) */
+  int64_t xcd_heads;
 } vafa_plan_info;
 
 /* Plan for packed_varlen_attn (fa/interface.py:184-236, 293-338).

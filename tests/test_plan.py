@@ -240,6 +240,14 @@ def expected_tiles(q_lens, k_lens, D):
     return q, k
 
 
+def expected_xcd_heads(q_lens, k_lens):
+    """Forward grid with an item's heads on one XCD when most of the work lies
+    in segments of at most 128 queries."""
+    lq, lk = np.asarray(q_lens, dtype=np.float64), np.asarray(k_lens, dtype=np.float64)
+    w = lq * lk
+    return int(w.sum() > 0 and 2 * w[lq > 128].sum() < w.sum())
+
+
 @pytest.mark.parametrize("q_lens,k_lens", [
     ([200, 300], [150, 250]),        # long segments: wide tiles at D <= 128 / D = 128
     ([3, 16, 1], [5000, 900, 40]),   # decode-shaped: 128-row tiles, 256-key tiles at D=128
@@ -252,6 +260,7 @@ def expected_tiles(q_lens, k_lens, D):
 def test_varlen_tile_choice(q_lens, k_lens, D):
     p = check_varlen_plan(q_lens, k_lens, H=2, D=D)
     assert (p.info.q_tile, p.info.k_tile) == expected_tiles(q_lens, k_lens, D)
+    assert p.info.xcd_heads == expected_xcd_heads(q_lens, k_lens)
 
 
 def test_varlen_tile_choice_on_configs():
@@ -259,6 +268,8 @@ def test_varlen_tile_choice_on_configs():
     c2, c3 = W.config2(0), W.config3(0)
     assert expected_tiles(c2.q_lens, c2.k_lens, c2.D) == (256, 256)
     assert expected_tiles(c3.q_lens, c3.k_lens, c3.D) == (128, 256)
+    assert expected_xcd_heads(c2.q_lens, c2.k_lens) == 0
+    assert expected_xcd_heads(c3.q_lens, c3.k_lens) == 1
 
 
 def test_varlen_plan_split_counts_match_reference_rule():

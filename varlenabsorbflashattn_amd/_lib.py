@@ -39,7 +39,7 @@ class PlanInfo(C.Structure):
         "off_fwd", "n_fwd", "off_comb", "n_comb", "off_kv", "n_kv", "off_qt", "n_qt",
         "n_part_rows", "plan_ints", "q_tile", "k_tile", "max_split", "max_comb_rows", "n_kv_res",
         "off_dq", "n_dq", "off_dqc", "n_dqc", "max_dqc_rows", "off_fkv", "n_fkv",
-        "off_fcomb", "n_fcomb", "n_fpart_rows", "max_fcomb_rows")]
+        "off_fcomb", "n_fcomb", "n_fpart_rows", "max_fcomb_rows", "xcd_heads")]
 
 
 _lib = None

@@ -516,6 +516,7 @@ static int varlen_fwd_impl(const void *q, const void *k, const void *v, void *o,
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
+  a.xcd_heads = (int)info->xcd_heads;
   if (pad) {
     launch_pad16(q, w.pq, info->T_q * info->H, st);
     launch_pad16(k, w.pk, info->T_k * info->H, st);
@@ -592,6 +593,7 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv;
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
+  a.xcd_heads = (int)info->xcd_heads;
   a.stage = stage;
   if (pad) {
     const int64_t rq = info->T_q * info->H, rk = info->T_k * info->H;

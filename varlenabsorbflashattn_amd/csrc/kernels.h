@@ -20,6 +20,7 @@ struct VarlenArgs {
   int64_t T_q;
   int H, D;
   int q_tile, k_tile;  // the plan's tiles: forward / dQ rows and dK/dV keys per workgroup
+  int xcd_heads;       // forward grid: an item's H workgroups on one XCD (1) or item-major
   float scale;
   int stage;  // backward stage (VAFA_BWD_*) or -1 for all
   // the matrix-core dQ kernel computes delta from O and dO itself and writes

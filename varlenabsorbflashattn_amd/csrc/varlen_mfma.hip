@@ -220,14 +220,26 @@ template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     T *__restrict__ o, float *__restrict__ lse, float *__restrict__ part_o,
-    float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, float c) {
+    float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, float c,
+    int n_items, int xcd_heads) {
   using M = Mfma<T>;
   constexpr int NC = D / 16;   // 16-wide d chunks (S^T reduction)
   constexpr int ND = D / 32;   // 32-row d tiles of O^T
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
-  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  // grid: item-major with heads innermost, or (xcd_heads) the H workgroups of
+  // an item on one XCD -- workgroup b runs on XCD b % kXcds
+  int item, h;
+  if (xcd_heads) {
+    const int grp = blockIdx.x / (kXcds * H), rr = blockIdx.x % (kXcds * H);
+    item = grp * kXcds + rr % kXcds;
+    h = rr / kXcds;
+    if (item >= n_items) return;  // padding of the last group
+  } else {
+    item = blockIdx.x / H;
+    h = blockIdx.x % H;
+  }
   const PlanItem it = load_item(items, item);
   const int q0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -322,9 +334,12 @@ void launch_fwd_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = FwdSmem<D>::kBytes;
   hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D, NW>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  hipLaunchKernelGGL((varlen_fwd_kernel<T, D, NW>), dim3((unsigned)(a.n_items * a.H)),
-                     dim3(64 * NW), smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
-                     (T *)a.o, a.lse, a.part_o, a.part_lse, a.items, a.H, a.scale * kLog2e);
+  const int64_t n_wg = a.xcd_heads ? (a.n_items + kXcds - 1) / kXcds * kXcds * a.H
+                                   : a.n_items * a.H;
+  hipLaunchKernelGGL((varlen_fwd_kernel<T, D, NW>), dim3((unsigned)n_wg), dim3(64 * NW), smem,
+                     st, (const T *)a.q, (const T *)a.k, (const T *)a.v, (T *)a.o, a.lse,
+                     a.part_o, a.part_lse, a.items, a.H, a.scale * kLog2e, (int)a.n_items,
+                     a.xcd_heads);
 }
 
 // The plan's query tile sets the workgroup: 32 rows per wave.

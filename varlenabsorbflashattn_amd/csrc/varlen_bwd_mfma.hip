@@ -31,27 +31,54 @@ namespace vafa {
 namespace {
 
 constexpr int kRB = 32;  // rows per staged block (queries for dK/dV, keys for dQ)
-// LDS row padding (elements): these tiles are read both as rows and
-// transposed; a sweep of 8/16/24/32 picked 24
-constexpr int kPad = 24;
+// LDS layout of a 32-row tile of 16-bit rows that is read both as rows
+// (ds_read_b128: 16 lanes take one 16-byte chunk of 16 consecutive rows) and
+// transposed (ds_read_b64_tr_b16: 32 lanes take 64 bytes of 4 consecutive
+// rows).  With one row stride the two cannot both be conflict-free -- row
+// reads want 4 x odd dwords, transposed reads 16 mod 64 dwords -- so rows sit
+// in groups of four: P1 elements apart inside a group (P1/2 dwords = 16 mod
+// 32: the 4 row pieces of a transposed read fill distinct banks) and P2 =
+// 4*P1 + 8 elements from group to group (4 dwords past a multiple of the 64
+// banks: 16 consecutive rows start on 16 distinct 4-bank groups).  The
+// operand reads add row offsets that are multiples of 4 rows to a per-lane
+// base, so those stay compile-time immediates.
+template <int D>
+struct GTile {
+  static constexpr int P1 = (D / 2) % 32 == 16 ? D : D + 32;
+  static constexpr int P2 = 4 * P1 + 8;
+  static constexpr int kElems = (kRB / 4) * P2;  // 32 rows
+  static __device__ __forceinline__ int row(int r) { return (r >> 2) * P2 + (r & 3) * P1; }
+};
+
+// A operand of a 32x32x16 MFMA read transposed from a GTile (columns c0 +
+// l % 32 as the row index, tile rows k0 .. k0+15 as the reduction index in
+// the relabelled order of the C layout; k0 a multiple of 4), as tr_operand
+// does for a fixed row stride.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::v8 tr_operand_g(const T *tile, int k0, int c0,
+                                                             int lane) {
+  using L = GTile<D>;
+  const int i = lane & 15, g = lane >> 4;
+  const T *p = tile + (k0 >> 2) * L::P2 + L::row(4 * (g >> 1) + (i >> 2)) + c0 + (g & 1) * 16 +
+               4 * (i & 3);
+  return as_v8<T>(join(lds_tr16(p), lds_tr16(p + 2 * L::P2)));
+}
 
 template <int D>
 struct DkvSmem {
-  static constexpr int RS = D + kPad;
-  static constexpr int kQs = kRB * RS;                        // Q (or dO) row-major
+  static constexpr int kQs = GTile<D>::kElems;                // Q (or dO) rows
   static constexpr int kBufBytes = 2 * kQs * 2 + 2 * kRB * 4;  // Q, dO, LSE, delta
   static constexpr int kBytes = 2 * kBufBytes;
 };
 
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
-// past r_end read as zero) into a padded [32][RS] block: wave w of NW moves
+// past r_end read as zero) into a GTile block: wave w of NW moves
 // rows RPW*w .. RPW*w + RPW-1 (RPW = 32/NW), one instruction per row with
 // lanes < D/8 active.  One buffer descriptor covers the block's valid rows;
 // the row sits in the lane offset.
 template <typename T, int D, int NW>
 __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H, int h,
                                          uint32_t base, int wave, int lane) {
-  constexpr int RS = D + kPad;
   constexpr int RPW = kRB / NW;
   const int rows = uniform_clamp(r_end - r0, kRB);
   const u32x4 rs = rsrc_words32(src + (int64_t)r0 * H * D, (uint32_t)(rows * H * D * 2));
@@ -62,7 +89,7 @@ __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H,
       // one add of a scalar row term (volatile: not hoisted into RPW registers)
       int voff;
       asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(n * H * D * 2), "v"(off));
-      lds_dma16(rs, base + (wave * RPW + n) * RS * 2, voff);
+      lds_dma16(rs, base + GTile<D>::row(wave * RPW + n) * 2, voff);
     }
   }
 }
@@ -75,7 +102,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     float scale) {
   using M = Mfma<T>;
   using S = DkvSmem<D>;
-  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  using L = GTile<D>;
+  constexpr int NC = D / 16, ND = D / 32;
   constexpr int kPre = D >= 128 ? 2 : 4;  // operand ring depth within the register budget
   // At D=256 two workgroups share a key tile, each accumulating dK/dV for one
   // half of d (S and dP still over all of d): the full-width accumulators did
@@ -136,8 +164,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
 
   // per-lane element offsets: row lrow at d = 8*lhalf (A of S and dP) and the
   // origin of the transposed reads (layout of tr_operand)
-  const int a_off = lrow * RS + lhalf * 8;
-  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+  const int a_off = L::row(lrow) + lhalf * 8;
+  const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
                     4 * (lane & 3);
   for (int j = 0; j < nblk; ++j) {
     wait_vmcnt<0>();
@@ -172,8 +200,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       // else Q^T (for dK^T, with dS)
       auto top = [&](int i) {
         const lds_cptr<T> p = (((i / NDO) & 1) ? qs : ds_) + t_off +
-                              ((i / NDO) >> 1) * 16 * RS + (dpart * NDO + i % NDO) * 32;
-        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+                              ((i / NDO) >> 1) * 4 * L::P2 + (dpart * NDO + i % NDO) * 32;
+        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 2 * L::P2)));
       };
       typename M::v8 tring[kPre];
   #pragma unroll
@@ -286,13 +314,13 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
 // sum_combine_kernel adds in chunk order.
 template <int D>
 struct FusedSmem {
-  static constexpr int RS = D + kPad;
-  static constexpr int kQOff = 0;                     // Q block [32][RS]
-  static constexpr int kDoOff = kRB * RS * 2;         // dO block [32][RS]
-  static constexpr int kLsOff = 2 * kRB * RS * 2;     // LSE [32], delta [32]
-  static constexpr int kROff = kLsOff + 2 * kRB * 4;  // K rows, later the dQ^T sums
+  static constexpr int kTile = GTile<D>::kElems;
+  static constexpr int kQOff = 0;                     // Q block (GTile)
+  static constexpr int kDoOff = kTile * 2;            // dO block (GTile)
+  static constexpr int kLsOff = 2 * kTile * 2;        // LSE [32], delta [32]
+  static constexpr int kROff = kLsOff + 2 * kRB * 4;  // K rows (a GTile per wave), later the dQ^T sums
   static constexpr int kRS = D + 4;                   // fp32 row stride of the sums
-  static constexpr int kKtBytes = 4 * 32 * RS * 2;
+  static constexpr int kKtBytes = 4 * kTile * 2;
   static constexpr int kRedBytes = 4 * 32 * kRS * 4;
   static constexpr int kDsS = 40;                     // dS^T [32 keys][40]
   static constexpr int kDsOff = kROff + (kKtBytes > kRedBytes ? kKtBytes : kRedBytes);
@@ -308,7 +336,8 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
   using M = Mfma<T>;
   using S = FusedSmem<D>;
   using v8 = typename M::v8;
-  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  using L = GTile<D>;
+  constexpr int NC = D / 16, ND = D / 32;
   constexpr int kPre = 4;
   static_assert(D <= 64, "the fused kernel serves D <= 64");
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -362,10 +391,10 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
   const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(smem_raw + S::kQOff));
   const lds_cptr<T> ds_ = as_lds(reinterpret_cast<const T *>(smem_raw + S::kDoOff));
   const float *ls = reinterpret_cast<const float *>(smem_raw + S::kLsOff);
-  T *kt = reinterpret_cast<T *>(smem_raw + S::kROff) + wave * 32 * RS;
+  T *kt = reinterpret_cast<T *>(smem_raw + S::kROff) + wave * S::kTile;
   T *dst = reinterpret_cast<T *>(smem_raw + S::kDsOff) + wave * 32 * S::kDsS;
-  const int a_off = lrow * RS + lhalf * 8;
-  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+  const int a_off = L::row(lrow) + lhalf * 8;
+  const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
                     4 * (lane & 3);
   const int ntile = (k1 - k0 + 127) / 128;
   wait_vmcnt<0>();
@@ -379,12 +408,12 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
     // transposed (LDS operations of one wave execute in order)
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
-      *reinterpret_cast<v8 *>(kt + lrow * RS + cc * 16 + lhalf * 8) = kf[cc];
+      *reinterpret_cast<v8 *>(kt + L::row(lrow) + cc * 16 + lhalf * 8) = kf[cc];
     v8 ktf[2 * ND];
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) ktf[hk * ND + dt] = tr_operand<T>(kt, RS, 16 * hk, 32 * dt, lane);
+      for (int dt = 0; dt < ND; ++dt) ktf[hk * ND + dt] = tr_operand_g<T, D>(kt, 16 * hk, 32 * dt, lane);
     // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
     auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
     f32x16 s, dp;
@@ -444,8 +473,8 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
       for (int r = 0; r < 16; ++r) adk[i][r] = adv[i][r] = 0.f;
     auto top = [&](int i) {
       const lds_cptr<T> p =
-          (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 16 * RS + (i % ND) * 32;
-      return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+          (((i / ND) & 1) ? qs : ds_) + t_off + ((i / ND) >> 1) * 4 * L::P2 + (i % ND) * 32;
+      return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 2 * L::P2)));
     };
     v8 tring[kPre];
 #pragma unroll
@@ -554,20 +583,19 @@ __device__ __forceinline__ void load_rows(Rows<D, NT> &s, const T *__restrict__ 
 }
 
 template <typename T, int D, int NT>
-__device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int RS, int t) {
+__device__ __forceinline__ void store_rows(const Rows<D, NT> &s, T *dst, int t) {
   constexpr int CPR = D / 8;
 #pragma unroll
   for (int i = 0; i < Rows<D, NT>::kPer; ++i) {
     const int ci = t + NT * i;
     if (ci < Rows<D, NT>::kChunks)
-      *reinterpret_cast<u32x4 *>(dst + (ci / CPR) * RS + (ci % CPR) * 8) = s.v[i];
+      *reinterpret_cast<u32x4 *>(dst + GTile<D>::row(ci / CPR) + (ci % CPR) * 8) = s.v[i];
   }
 }
 
 template <int D>
 struct DqSmem {
-  static constexpr int RS = D + kPad;
-  static constexpr int kKs = kRB * RS;
+  static constexpr int kKs = GTile<D>::kElems;
   static constexpr int kBuf = 2 * kKs;  // K and V row-major
   static constexpr int kBytes = 2 * kBuf * 2;
 };
@@ -580,7 +608,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     const int32_t *__restrict__ items, int H, float c, float scale) {
   using M = Mfma<T>;
   using S = DqSmem<D>;
-  constexpr int NC = D / 16, ND = D / 32, RS = S::RS;
+  using L = GTile<D>;
+  constexpr int NC = D / 16, ND = D / 32;
   constexpr int kPre = 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
@@ -607,7 +636,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   Rows<D, NS> stg;
   auto put = [&](int buf) {
     T *ks = smem + buf * S::kBuf;
-    store_rows<T, D, NS>(stg, stage_k ? ks : ks + S::kKs, RS, st);
+    store_rows<T, D, NS>(stg, stage_k ? ks : ks + S::kKs, st);
   };
   const int nblk = (k1 - k0 + kRB - 1) / kRB;
   if (nblk > 0) load_rows<T, D, NS>(stg, src, k0, k1, H, h, st);
@@ -667,8 +696,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-  const int a_off = lrow * RS + lhalf * 8;
-  const int t_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 +
+  const int a_off = L::row(lrow) + lhalf * 8;
+  const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
                     4 * (lane & 3);
   if (nblk > 0) put(0);
   __syncthreads();
@@ -703,8 +732,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
       }
       // K^T operands of dQ^T: i -> d tile i % ND, key half i / ND
       auto top = [&](int i) {
-        const lds_cptr<T> p = ks + t_off + (i / ND) * 16 * RS + (i % ND) * 32;
-        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 8 * RS)));
+        const lds_cptr<T> p = ks + t_off + (i / ND) * 4 * L::P2 + (i % ND) * 32;
+        return as_v8<T>(join(lds_tr8<T>(p), lds_tr8<T>(p + 2 * L::P2)));
       };
       typename M::v8 tring[kPre];
 #pragma unroll

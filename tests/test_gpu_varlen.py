@@ -110,6 +110,38 @@ def test_varlen_input_scales(device, dist):
     assert_close("o", got[0], ref[0], rel=True)
 
 
+WIDE_CASES = [
+    # (q_lens, k_lens): long segments carry the work, so the plan takes
+    # 256-row query tiles, whose forward runs two 32-row blocks per wave
+    ([300, 130, 40], [5000, 64, 1]),     # split-K item, Lk = 64, one key
+    ([257, 200, 33], [63, 1, 65]),       # first tile is the tail tile; one-row item
+    ([520, 3], [700, 2000]),             # three query tiles per (segment, head)
+]
+
+
+@pytest.mark.parametrize("dist", [1.0, 8.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("case", range(len(WIDE_CASES)))
+def test_varlen_wide_tiles(device, case, D, dtype, dist):
+    """256-row query tiles (8-wave forward and dQ workgroups) at D = 64 / 128,
+    bf16 and fp16: split-K items, one-key and tail-only items, partial waves.
+    At dist = 8 (scores scaled 64x, fa-tools/benchmark_packed_varlen_flash_attn.py:226-233)
+    later key tiles raise the running max far above the first tile's, so the
+    lazy rescale runs on most tiles."""
+    from varlenabsorbflashattn_amd import _lib
+    q_lens, k_lens = WIDE_CASES[case]
+    plan = _lib.plan_varlen(cu_from_lens(q_lens).numpy(), cu_from_lens(k_lens).numpy(), 4, D)
+    assert plan.info.q_tile == 256
+    print(f"[varlen wide] q={q_lens} k={k_lens} D={D} {dtype} dist={dist}", flush=True)
+    got, ref = run_case(q_lens, k_lens, 4, D, dtype, device, dist_scale=dist)
+    rel = dist > 1.0  # near one-hot rows: see test_varlen_input_scales
+    for name, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        if dist > 1.0 and name != "o":
+            continue  # gradients of the 64x scores are checked by the backward tests
+        assert_close(name, a, r, rel=rel)
+
+
 def test_single_key_returns_v(device):
     """Lk = 1: softmax weight 1 -> O == V exactly; dq = dk = 0 up to fp32 rounding
     (delta = O.dO and dP = dO.V are summed in different orders)."""

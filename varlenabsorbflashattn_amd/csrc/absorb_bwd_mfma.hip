@@ -61,8 +61,11 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
     dma_block<FP, kDuWaves, S::XS>(X + (int64_t)kb * F, (uint32_t)(rows * F * 2), F,
                             lds_addr(smem + buf * S::kTile), wave, lane);
   };
+  // only tiles of the key range are fetched (a tile past it would land as
+  // zeros and cost a tile's DMA instructions)
 #pragma unroll
-  for (int b = 0; b < kNBuf - 1; ++b) issue(k0 + b * kBK, b);
+  for (int b = 0; b < kNBuf - 1; ++b)
+    if (b < nt) issue(k0 + b * kBK, b);
 
   // U^T and dAX^T fragments (B operands of S^T and dP^T), rows past the tile zero
   v8 uf[NK], gf[NK];
@@ -102,9 +105,14 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
   constexpr int NA = 2 * NK;  // A reads of S^T / dP^T per tile
   int buf = 0;                // j % kNBuf
   for (int j = 0; j < nt; ++j) {
-    wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    // tile j landed (tile j+1, if there is one, may still be in flight)
+    static_assert(kNBuf == 3, "one tile in flight behind the current one");
+    if (j + 1 < nt)
+      wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
-    issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
+    if (j + kNBuf - 1 < nt) issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
     const int kb = k0 + j * kBK;
     if (wave_active) {
       const lds_cptr<T> xa = as_lds(smem + buf * S::kTile + a_off);

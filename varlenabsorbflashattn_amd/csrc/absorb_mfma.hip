@@ -83,8 +83,11 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
     dma_block<FP, kFwdWaves, S::XS>(X + (int64_t)kb * F, (uint32_t)(rows * F * 2), F,
                              lds_addr(smem + buf * S::kTile), wave, lane);
   };
+  // only tiles of the key range are fetched (a tile past it would land as
+  // zeros and cost a tile's DMA instructions)
 #pragma unroll
-  for (int b = 0; b < kNBuf - 1; ++b) issue(k0 + b * kBK, b);
+  for (int b = 0; b < kNBuf - 1; ++b)
+    if (b < nt) issue(k0 + b * kBK, b);
 
   // U^T fragments (B operand of S^T = X U^T): row `row`, f = 32*kc + 8*lq + t
   v8 uf[NK];
@@ -118,11 +121,16 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   const int t_off = (4 * lq + (l16 >> 2)) * S::XS + 4 * (l16 & 3);
   int buf = 0;  // j % kNBuf
   for (int j = 0; j < nt; ++j) {
-    // tile j landed (later tiles may still be in flight), visible to all waves,
-    // and every wave is done with tile j-1 whose slot is refilled next
-    wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    // tile j landed (tile j+1, if there is one, may still be in flight),
+    // visible to all waves, and every wave is done with tile j-1 whose slot
+    // is refilled next
+    static_assert(kNBuf == 3, "one tile in flight behind the current one");
+    if (j + 1 < nt)
+      wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
-    issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
+    if (j + kNBuf - 1 < nt) issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
     const int kb = k0 + j * kBK;
     if (wave_active) {
       const lds_cptr<T> xa = as_lds(smem + buf * S::kTile + a_off);

@@ -613,8 +613,7 @@ __global__ __launch_bounds__(64) void absorb_dax_kernel(const T *__restrict__ dO
 template <typename T, int FP>
 void launch_du_fp(const AbsorbArgs &a, hipStream_t st) {
   const int smem = AbsSmem<FP>::kLoopBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_du_kernel<T, FP>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_du_kernel<T, FP>), smem);
   hipLaunchKernelGGL((absorb_du_kernel<T, FP>), dim3((unsigned)a.n_qseg), dim3(64 * kDuWaves), smem,
                      st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in, a.delta,
                      (T *)a.du, a.ax, a.qseg_items, a.H, a.F, a.scale * kLog2e, a.scale);
@@ -628,15 +627,13 @@ void launch_dx_fp(const AbsorbArgs &a, hipStream_t st) {
   // of the other kind
   const int64_t n_res = a.n_kv_res, n_str = a.n_kv - a.n_kv_res;
   if (n_res > 0) {
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_res_kernel<T, FP>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_dx_res_kernel<T, FP>), smem);
     hipLaunchKernelGGL((absorb_dx_res_kernel<T, FP>), dim3((unsigned)n_res), dim3(64 * kDxWaves),
                        smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
                        a.delta, (T *)a.dX, a.kv_items, a.H, a.F, a.scale * kLog2e, a.scale);
   }
   if (n_str > 0) {
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>), smem);
     hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)n_str), dim3(64 * kDxWaves),
                        smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
                        a.delta, (T *)a.dX, a.kv_items + n_res * 8, a.H, a.F,

@@ -538,8 +538,7 @@ __global__ __launch_bounds__(256, 2) void absorb_dx_f32_kernel(
 template <int FP>
 void launch_fwd_fp(const AbsorbArgs &a, const float *wvt, hipStream_t st) {
   const int smem = F32Smem<FP>::kFwdBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_fwd_f32_kernel<FP>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_f32_kernel<FP>), smem);
   hipLaunchKernelGGL(absorb_fwd_f32_kernel<FP>, dim3((unsigned)a.n_items), dim3(256), smem, st,
                      (const float *)a.u, (const float *)a.X, wvt, (float *)a.O, a.lse, a.part_o,
                      a.part_lse, a.items, a.H, a.F, a.DH, a.scale * kLog2e);
@@ -549,8 +548,7 @@ template <int FP>
 void launch_bwd_fp(const AbsorbArgs &a, hipStream_t st) {
   if (a.n_qseg > 0) {
     const int smem = F32Smem<FP>::kFwdBytes;
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_du_f32_kernel<FP>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_du_f32_kernel<FP>), smem);
     hipLaunchKernelGGL(absorb_du_f32_kernel<FP>, dim3((unsigned)a.n_qseg), dim3(256), smem, st,
                        (const float *)a.u, (const float *)a.X, a.lse_in, a.delta,
                        (const float *)a.dax, (float *)a.du, a.ax, a.qseg_items, a.H, a.F,
@@ -558,8 +556,7 @@ void launch_bwd_fp(const AbsorbArgs &a, hipStream_t st) {
   }
   if (a.n_kv > 0) {
     const int smem = F32Smem<FP>::kDxBytes;
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dx_f32_kernel<FP>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_dx_f32_kernel<FP>), smem);
     hipLaunchKernelGGL(absorb_dx_f32_kernel<FP>, dim3((unsigned)a.n_kv), dim3(256), smem, st,
                        (const float *)a.u, (const float *)a.X, a.lse_in, a.delta,
                        (const float *)a.dax, (float *)a.dX, a.kv_items, a.H, a.F,

@@ -272,8 +272,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   const int smem = AbsSmem<FP>::kLoopBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>), smem);
   hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(64 * kFwdWaves),
                      smem, st, (const T *)a.u, (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o,
                      a.part_lse, a.items, a.H, a.F, a.scale * kLog2e);

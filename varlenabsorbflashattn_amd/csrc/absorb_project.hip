@@ -457,14 +457,12 @@ void wgrad_fp(const Wgrad &p, hipStream_t st) {
   if (wgs == 0) return;
   constexpr int smem = WgSmem<FP>::kBytes;
   if (p.dq != nullptr) {
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&wgrad_kernel<T, FP, true>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&wgrad_kernel<T, FP, true>), smem);
     hipLaunchKernelGGL((wgrad_kernel<T, FP, true>), dim3((unsigned)wgs), dim3(256), smem, st,
                        (const T *)p.A, (const T *)p.B, (const T *)p.Wt, (T *)p.dq, p.part, p.T_q,
                        p.tchunk, p.G, p.F, p.DH, n_db);
   } else {
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&wgrad_kernel<T, FP, false>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&wgrad_kernel<T, FP, false>), smem);
     hipLaunchKernelGGL((wgrad_kernel<T, FP, false>), dim3((unsigned)wgs), dim3(256), smem, st,
                        (const T *)p.A, (const T *)p.B, nullptr, nullptr, p.part, p.T_q,
                        p.tchunk, p.G, p.F, p.DH, n_db);

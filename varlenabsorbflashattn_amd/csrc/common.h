@@ -131,6 +131,13 @@ __device__ __forceinline__ int uniform_clamp(int n, int hi) {
   return __builtin_amdgcn_readfirstlane(n);
 }
 
+// LDS-DMA (buffer_load ... lds) takes its LDS base in M0, which the asm
+// below writes.  M0 is a reserved register, so clang ignores it in a clobber
+// list (and warns, silenced here); this is sound only while compiler code in
+// these kernels never keeps a value in M0, which tests/test_abi.py checks in
+// the generated assembly of every source that uses these helpers.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t lds_base, int32_t voff) {
   // (an ext_vector_type operand is what binds to an SGPR quad under "s")
   typedef uint32_t sgpr4 __attribute__((ext_vector_type(4)));
@@ -159,6 +166,7 @@ __device__ __forceinline__ void lds_dma4(u32x4 r, uint32_t lds_base, int32_t vof
                : "s"(lds_base), "v"(voff), "s"(q)
                : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // 32-bit LDS address of a pointer into __shared__ memory.
 template <typename P>

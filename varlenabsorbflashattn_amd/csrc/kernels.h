@@ -6,6 +6,15 @@
 
 namespace vafa {
 
+// Lets kernel `fn` be launched with `bytes` of dynamic LDS (above the 64 KB
+// default).  A failure is not returned here: HIP keeps it as the thread's
+// last error, so the launch that follows fails and every entry point reports
+// it through check_launch (hipGetLastError) as VAFA_ERR_RUNTIME.
+inline void allow_dynamic_lds(const void *fn, int bytes) {
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)e;
+}
+
 struct VarlenArgs {
   const void *q, *k, *v, *o_in, *dout;
   void *o, *dq, *dk, *dv;

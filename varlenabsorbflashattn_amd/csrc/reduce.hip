@@ -531,8 +531,7 @@ void dwv_lds(const AbsorbArgs &a, hipStream_t st) {
   const int64_t wgs = a.n_tchunks * a.H * n_db;
   if (wgs > 0) {
     constexpr int smem = DwSmem<FP>::kBytes;
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&absorb_dwv_lds_kernel<T, FP>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_dwv_lds_kernel<T, FP>), smem);
     hipLaunchKernelGGL((absorb_dwv_lds_kernel<T, FP>), dim3((unsigned)wgs), dim3(256), smem, st,
                        a.ax, (const T *)a.dO, a.dwv_part, a.T_q, a.tchunk, a.H, a.F, a.DH, n_db);
   }

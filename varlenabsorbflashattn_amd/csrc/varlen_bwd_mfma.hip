@@ -801,8 +801,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 template <typename T, int D, int NW>
 void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = DkvSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, NW>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, NW>), smem);
   const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
   hipLaunchKernelGGL((varlen_dkv_kernel<T, D, NW>),
                      dim3((unsigned)(a.n_kv * a.H * dsplit)), dim3(64 * NW), smem, st,
@@ -825,8 +824,7 @@ template <typename T, int D>
 void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_fkv == 0) return;
   const int smem = FusedSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fkv_kernel<T, D>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_fkv_kernel<T, D>), smem);
   hipLaunchKernelGGL((varlen_fkv_kernel<T, D>), dim3((unsigned)(a.n_fkv * a.H)), dim3(256),
                      smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.fkv_items, a.H,
@@ -836,8 +834,7 @@ void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
 template <typename T, int D, int NW>
 void launch_dq_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = DqSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_dq_kernel<T, D, NW>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dq_kernel<T, D, NW>), smem);
   hipLaunchKernelGGL((varlen_dq_kernel<T, D, NW>), dim3((unsigned)(a.n_items * a.H)),
                      dim3(64 * NW), smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,
                      (const T *)a.dout, a.lse_in, a.delta,

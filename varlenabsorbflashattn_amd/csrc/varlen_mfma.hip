@@ -332,8 +332,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
 template <typename T, int D, int NW>
 void launch_fwd_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = FwdSmem<D>::kBytes;
-  hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D, NW>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D, NW>), smem);
   const int64_t n_wg = a.xcd_heads ? (a.n_items + kXcds - 1) / kXcds * kXcds * a.H
                                    : a.n_items * a.H;
   hipLaunchKernelGGL((varlen_fwd_kernel<T, D, NW>), dim3((unsigned)n_wg), dim3(64 * NW), smem,

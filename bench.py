@@ -50,8 +50,9 @@ def stats(ms):
             "p50": pct(0.5), "p90": pct(0.9), "min": xs[0], "max": xs[-1], "n": len(xs)}
 
 
-def timed(fn, iters, warmup=1):
-    """Run fn() warmup times, then iters times with a HIP event pair around
+def timed(fn, iters, warmup=3):
+    """Run fn() warmup times (the first calls after a change of workload run
+    at a lower shader clock), then iters times with a HIP event pair around
     each call, recorded on torch's current stream (the stream the C ABI
     launches on).  Returns the stats of the per-call ms."""
     import torch

@@ -91,11 +91,13 @@ HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 2
                (2, 16, 50)]  # d_kv not a multiple of 8: the wave-per-row path
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "f16", "f32"])
 @pytest.mark.parametrize("H,D_H,d_kv", HEAD_SHAPES, ids=[f"H{h}_DH{d}_F{f}" for h, d, f in HEAD_SHAPES])
 def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
-    """Matrix-core paths (bf16 and fp32) at head counts, head dims and feature
-    widths off the benchmark shape; d_kv = 50 takes the wave-per-row path."""
+    """Matrix-core paths (bf16, fp16 and fp32) at head counts, head dims and
+    feature widths off the benchmark shape; d_kv = 50 takes the wave-per-row
+    path."""
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)

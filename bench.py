@@ -609,7 +609,11 @@ def main():
                      "frac": dkv_tflops / BF16_PEAK_TFLOPS, "traffic": roofline_traffic(),
                      "work_per_launch": "8*H*D*sum(L^2) = %.4g FLOP" % dkv_flops,
                      "ms_per_launch": dkv_st["mean"], "ms_stats": dkv_st,
-                     "timing": "HIP events on the launch stream around each dK/dV launch"},
+                     "timing": "HIP events on the launch stream around each dK/dV launch",
+                     "traffic_source": "rocprofv3 FETCH_SIZE x fetch_factor + WRITE_SIZE x "
+                                       "write_factor of this kernel on this workload, recorded "
+                                       "with the commands in profiles/roofline_traffic.json "
+                                       "(bench.py cannot read counters itself)"},
         "c2": c2,
         "secondary": secondary,
         "cpu_baseline": cpu,

@@ -88,7 +88,8 @@ def test_absorb_bf16_parity(device, name, q_lens, k_lens):
 # head counts and head dims off the benchmark shape (rows of a workgroup are
 # laid out head-major, 64 / H tokens per head)
 HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 216),
-               (2, 16, 50)]  # d_kv not a multiple of 8: the wave-per-row path
+               (2, 16, 50),   # d_kv not a multiple of 8: the wave-per-row path
+               (6, 32, 96)]   # H not dividing 64: the wave-per-row path
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32],

@@ -142,6 +142,23 @@ def test_varlen_wide_tiles(device, case, D, dtype, dist):
         assert_close(name, a, r, rel=rel)
 
 
+@pytest.mark.parametrize("H,q_lens,k_lens,D", [
+    (3, [300, 5, 140], [200, 3000, 150], 64),     # 256-row tiles, item-major grid
+    (5, [3, 16, 1, 9], [3000, 1500, 1024, 40], 128),  # decode-shaped: an item's heads on one XCD
+    (7, [130, 20], [5000, 9000], 32),             # split-K items and their combine
+])
+def test_varlen_odd_head_counts(device, H, q_lens, k_lens, D):
+    """Head counts that are not multiples of the 8 XCDs, on both forward grid
+    layouts (the plan's xcd_heads flag), forward and backward."""
+    from varlenabsorbflashattn_amd import _lib
+    plan = _lib.plan_varlen(cu_from_lens(q_lens).numpy(), cu_from_lens(k_lens).numpy(), H, D)
+    print(f"[varlen odd H] H={H} q={q_lens} k={k_lens} D={D} xcd_heads={plan.info.xcd_heads}",
+          flush=True)
+    got, ref = run_case(q_lens, k_lens, H, D, torch.bfloat16, device)
+    for name, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(name, a, r)
+
+
 def test_single_key_returns_v(device):
     """Lk = 1: softmax weight 1 -> O == V exactly; dq = dk = 0 up to fp32 rounding
     (delta = O.dO and dP = dO.V are summed in different orders)."""

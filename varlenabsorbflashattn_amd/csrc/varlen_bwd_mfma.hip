@@ -110,6 +110,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   // not fit beside the K/V operands and spilled.
   constexpr int kDsplit = D >= 256 ? 2 : 1;
   constexpr int NDO = ND / kDsplit;  // 32-wide d tiles of dK/dV per workgroup
+  constexpr bool kDeltaInChain = D <= 64;
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int dpart = kDsplit > 1 ? (int)(blockIdx.x % kDsplit) : 0;
@@ -153,6 +154,14 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       // waited for here, in the prologue, not inside the loop
       asm volatile("" : "+v"(a), "+v"(b));
       kf[cc] = as_v8<T>(a);
+      // At D <= 64, V enters negated (an exact sign flip): the dP chain below
+      // starts from delta and yields delta - dP, so dS = P (dP - delta) is
+      // one multiply with a negated operand.  (At D = 128 the delta reads in
+      // front of the chain cost more than the subtractions they remove.)
+      if constexpr (kDeltaInChain) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) b[w] ^= 0x80008000u;
+      }
       vf[cc] = as_v8<T>(b);
     }
   }
@@ -176,11 +185,23 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
       const lds_cptr<T> ds_ = qs + S::kQs;
       const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
-      // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows)
+      // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows);
+      // with kDeltaInChain delta - dP = delta + dO (-V)^T, the chain starting
+      // from the block's delta (row r of the accumulator is query
+      // 8*(r/4) + 4*lhalf + r%4)
       auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
       f32x16 s, dp;
   #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 d4 = kDeltaInChain
+                             ? *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[4 * g + e] = 0.f;
+          dp[4 * g + e] = d4[e];
+        }
+      }
       u32x4 ring[kPre];
   #pragma unroll
       for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
@@ -206,24 +227,32 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       typename M::v8 tring[kPre];
   #pragma unroll
       for (int i = 0; i < kPre; ++i) tring[i] = top(i);
-      // P = exp2(S*c - LSE) and dS = P (dP - delta) per accumulator row r
-      // (query 8*(r/4) + 4*lhalf + r%4 of the block); keys past k1 have zero K
-      // and V rows, their dK / dV columns are never stored, so their P needs no
-      // masking.
+      // P = exp2(S*c - LSE) and dS = P (dP - delta) (= -(P (delta - dP))
+      // with kDeltaInChain) per accumulator row r (query 8*(r/4) + 4*lhalf +
+      // r%4 of the block); keys past k1 have zero K and V rows, their dK / dV
+      // columns are never stored, so their P needs no masking.
+      auto ds_of = [&](float p, float acc, float dl) {
+        if constexpr (kDeltaInChain)
+          return -(p * acc);
+        else
+          return p * (acc - dl);
+      };
       typename M::v8 pb[2], sb[2];
       // rows 0..7 (first 16 queries) before the products; rows 8..15 are
       // computed under the first half of the chain, which only reads rows 0..7,
-      // their LSE / delta read one product ahead
+      // their LSE (and delta) read one product ahead
   #pragma unroll
       for (int g = 0; g < 2; ++g) {
         const f32x4 L = *reinterpret_cast<const f32x4 *>(ls + g * 8 + lhalf * 4);
-        const f32x4 Dl = *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
+        const f32x4 Dl = kDeltaInChain
+                             ? f32x4{0.f, 0.f, 0.f, 0.f}
+                             : *reinterpret_cast<const f32x4 *>(ls + kRB + g * 8 + lhalf * 4);
   #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = g * 4 + e;
           const float p = fast_exp2(__builtin_fmaf(s[r], c, -L[e]));
           s[r] = p;
-          dp[r] = p * (dp[r] - Dl[e]);
+          dp[r] = ds_of(p, dp[r], Dl[e]);
         }
       }
       pb[0] = pack8<T>(s, 0);
@@ -234,7 +263,9 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       constexpr int kRowsPer = 8 / kSteps;
       constexpr int kEvery = 2 * NDO / kSteps;
       auto lse_at = [&](int r) { return ls[(r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
-      auto del_at = [&](int r) { return ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)]; };
+      auto del_at = [&](int r) {
+        return kDeltaInChain ? 0.f : ls[kRB + (r >> 2) * 8 + lhalf * 4 + (r & 3)];
+      };
       float Ln[kRowsPer], Dn[kRowsPer];
   #pragma unroll
       for (int rr = 0; rr < kRowsPer; ++rr) Ln[rr] = lse_at(8 + rr), Dn[rr] = del_at(8 + rr);
@@ -265,7 +296,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
             const int r = 8 + g * kRowsPer + rr;
             const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lc[rr]));
             s[r] = p;
-            dp[r] = p * (dp[r] - Dc[rr]);
+            dp[r] = ds_of(p, dp[r], Dc[rr]);
           }
           if (g == kSteps - 1) {
             pb[1] = pack8<T>(s, 8);
@@ -690,6 +721,23 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     Dr = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
   }
   asm volatile("" : "+v"(Lr), "+v"(Dr));
+  // At D = 128 (registers to spare) the dO operands enter negated (an exact
+  // sign flip, after delta is formed from them) and the dP^T chain starts
+  // from a block holding this lane's delta: it yields delta - dP, and
+  // dS = P (dP - delta) is one multiply with a negated operand.
+  constexpr bool kDeltaInChain = D == 128;
+  f32x16 drb;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) drb[r] = kDeltaInChain ? Dr : 0.f;
+  if constexpr (kDeltaInChain) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      u32x4 w = __builtin_bit_cast(u32x4, dof[cc]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] ^= 0x80008000u;
+      dof[cc] = as_v8<T>(w);
+    }
+  }
   f32x16 acc[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i)
@@ -711,11 +759,12 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     if (wave_active) {
       const lds_cptr<T> ks = as_lds(smem + (j & 1) * S::kBuf);
       const lds_cptr<T> vs = ks + S::kKs;
-      // S^T = K Q^T (even reads, K rows) and dP^T = V dO^T (odd reads, V rows)
+      // S^T = K Q^T (even reads, K rows) and dP^T = V dO^T (odd reads, V
+      // rows; delta - dP^T when kDeltaInChain)
       auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? vs : ks) + a_off + (i >> 1) * 16); };
-      f32x16 s, dp;
+      f32x16 s, dp = drb;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
       u32x4 ring[kPre];
 #pragma unroll
       for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
@@ -742,7 +791,10 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(__builtin_fmaf(s[r], c, -Lr));
-        dp[r] = p * (dp[r] - Dr);
+        if constexpr (kDeltaInChain)
+          dp[r] = -(p * dp[r]);
+        else
+          dp[r] = p * (dp[r] - Dr);
       }
       if constexpr (decltype(masked)::value) {
         if (kb + kRB > k1) {

@@ -176,12 +176,15 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   const int a_off = L::row(lrow) + lhalf * 8;
   const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
                     4 * (lane & 3);
-  for (int j = 0; j < nblk; ++j) {
+  // Two query blocks per trip (below), so each block's LDS buffer is a
+  // compile-time offset folded into the LDS reads' immediates.
+  auto blk = [&](int j, auto bufc) {
+    constexpr int B = decltype(bufc)::value;
     wait_vmcnt<0>();
     __syncthreads();  // block j visible; every wave is done with the other buffer
-    if (j + 1 < nblk) issue(q0 + (j + 1) * kRB, (j + 1) & 1);
+    if (j + 1 < nblk) issue(q0 + (j + 1) * kRB, 1 - B);
     if (wave_active) {
-      const unsigned char *base = smem_raw + (j & 1) * S::kBufBytes;
+      const unsigned char *base = smem_raw + B * S::kBufBytes;
       const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
       const lds_cptr<T> ds_ = qs + S::kQs;
       const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
@@ -306,6 +309,10 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  };
+  for (int j = 0; j < nblk; j += 2) {
+    blk(j, std::integral_constant<int, 0>{});
+    if (j + 1 < nblk) blk(j + 1, std::integral_constant<int, 1>{});
   }
   wait_vmcnt<0>();
 
@@ -753,11 +760,14 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
   // columns of those keys masked: the loop body is instantiated twice so the
   // other blocks carry no per-element key compares (if-converted, they were
   // 48 VALU instructions per block).
-  auto block = [&](int j, auto masked) {
+  // bufc: the block's LDS buffer, a compile-time constant when the loop
+  // below is paired, else j & 1
+  auto block = [&](int j, auto masked, auto bufc) {
+    const int B = bufc;
     const int kb = k0 + j * kRB;
     if (j + 1 < nblk) load_rows<T, D, NS>(stg, src, kb + kRB, k1, H, h, st);
     if (wave_active) {
-      const lds_cptr<T> ks = as_lds(smem + (j & 1) * S::kBuf);
+      const lds_cptr<T> ks = as_lds(smem + B * S::kBuf);
       const lds_cptr<T> vs = ks + S::kKs;
       // S^T = K Q^T (even reads, K rows) and dP^T = V dO^T (odd reads, V
       // rows; delta - dP^T when kDeltaInChain)
@@ -814,12 +824,31 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (j + 1 < nblk) put((j + 1) & 1);
+    if (j + 1 < nblk) put(1 - B);
     __syncthreads();
   };
+  // At D >= 128 two blocks per trip, so each block's LDS buffer is a
+  // compile-time offset folded into the LDS reads' immediates (at D = 64 the
+  // paired body needs more registers than four waves per SIMD allow); the
+  // last block is the masked one.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
   int j = 0;
-  for (; j + 1 < nblk; ++j) block(j, std::false_type{});
-  if (j < nblk) block(j, std::true_type{});
+  if constexpr (D >= 128) {
+    for (; j + 2 < nblk; j += 2) {
+      block(j, std::false_type{}, I0{});
+      block(j + 1, std::false_type{}, I1{});
+    }
+    if (j + 1 < nblk) {
+      block(j, std::false_type{}, I0{});
+      block(j + 1, std::true_type{}, I1{});
+    } else if (j < nblk) {
+      block(j, std::true_type{}, I0{});
+    }
+  } else {
+    for (; j + 1 < nblk; ++j) block(j, std::false_type{}, j & 1);
+    if (j < nblk) block(j, std::true_type{}, j & 1);
+  }
 
   if (!row_ok) return;
   if (pbase < 0) {

@@ -11,6 +11,8 @@
 // max: a tile's row max is taken (one cross-lane register swap, lane l <->
 // l^32) only when the tile's P sum shows the running max is out of date, and
 // the row sum needs no exchange until the end.
+#include <type_traits>
+
 #include "kernels.h"
 #include "mfma.h"
 
@@ -281,17 +283,25 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
   }
   __syncthreads();
 
-  for (int j = 0; j < nt; ++j) {
+  // Two tiles per trip, so each tile's LDS buffer is a compile-time offset
+  // that folds into the LDS instructions' immediates (a run-time (j & 1)
+  // select cost address adds on every tile).
+  auto step = [&](int j, auto buf) {
+    constexpr int B = decltype(buf)::value;
     const int kbase = k0 + j * kBN;
     if (j + 1 < nt) load_tile<T, D, NT>(regs, k, v, kbase + kBN, k1, H, h, tid);
-    const T *ks = smem + (j & 1) * FwdSmem<D>::kBuf;
+    const T *ks = smem + B * FwdSmem<D>::kBuf;
     const T *vs = ks + FwdSmem<D>::kKs;
     if (wave_active) fwd_tile<T, D>(ks, vs, qf, acc, m_run, l_part, c, kbase, k1, lane);
     if (j + 1 < nt) {
-      T *nks = smem + ((j + 1) & 1) * FwdSmem<D>::kBuf;
+      T *nks = smem + (1 - B) * FwdSmem<D>::kBuf;
       store_tile<T, D, NT>(regs, nks, nks + FwdSmem<D>::kKs, tid);
     }
     __syncthreads();
+  };
+  for (int j = 0; j < nt; j += 2) {
+    step(j, std::integral_constant<int, 0>{});
+    if (j + 1 < nt) step(j + 1, std::integral_constant<int, 1>{});
   }
 
   if (!row_ok) return;

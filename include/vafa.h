@@ -175,13 +175,21 @@ VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const 
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  vafa_varlen_fwd with its workspace replaced by a static
  * device array of VAFA_NOALLOC_SCRATCH_BYTES per GPU, held until the process
- * ends: same arguments otherwise, same kernels, same results.  The caller
- * still passes inputs, outputs and the device plan.  Plans whose split
- * partials need more scratch than that return VAFA_ERR_WORKSPACE (use
- * vafa_varlen_fwd with a workspace).  Calls no hipMalloc/hipFree; the stream
- * must belong to the current device.  Every call on a GPU shares that GPU's
- * array, so calls that overlap on one GPU (other streams, other threads)
- * race: serialize them. */
+ * ends (it is part of the library's code object, so every GPU on which the
+ * library is loaded holds it, whether or not this entry point is called):
+ * same arguments otherwise, and the same kernels and results -- except for
+ * 16-bit D=16, which vafa_varlen_fwd runs on the D=32 matrix-core kernels
+ * over zero-padded copies in its workspace and this entry point runs on the
+ * wave-per-row kernels (no room for the copies): both are within the parity
+ * bound of the reference, not bit-identical.  The caller still passes inputs,
+ * outputs and the device plan.  Plans whose split partials need more scratch
+ * than that return VAFA_ERR_WORKSPACE (use vafa_varlen_fwd with a
+ * workspace).  Calls no hipMalloc/hipFree; the stream must belong to the
+ * current device.  The first call on a device looks the array's address up
+ * (hipGetSymbolAddress): make that call outside graph capture; later calls
+ * may be captured (no memset nodes are recorded).  Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other streams,
+ * other threads) race: serialize them. */
 #define VAFA_NOALLOC_SCRATCH_BYTES (64ll << 20)
 VAFA_API int vafa_varlen_fwd_noalloc(const void *q, const void *k, const void *v, void *o,
                                      float *lse, const int32_t *plan_dev,
@@ -227,6 +235,32 @@ VAFA_API int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, cons
                     int64_t D_H, int32_t dtype, float scale, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
+/* Workspace bytes needed by vafa_absorb_fwd_fold. */
+VAFA_API int64_t vafa_absorb_fwd_fold_workspace(const vafa_plan_info *info, int64_t D_KV,
+                                                int64_t D_H);
+
+/* 1 if vafa_absorb_fwd_fold takes this shape (16-bit dtype, H dividing 64 up
+ * to 8, D_KV a multiple of 8 padding onto one of the matrix-core widths up
+ * to 256, D_H in {16, 32, 64, 128}), else 0. */
+VAFA_API int vafa_absorb_fold_supported(int64_t H, int64_t D_KV, int64_t D_H, int32_t dtype);
+
+/* The forward of packed_target_attn from q_proj on, with the u projection
+ * folded into the attention kernel (replaces ta/interface.py:435 followed by
+ * _TargetAttnFunction.forward, ta/interface.py:153-223): from
+ * q_proj [T_q, H*D_H] (= q_raw W_Q, rounded to the 16-bit dtype, as
+ * vafa_absorb_project_fwd writes it with u = NULL), W_K [D_KV,H,D_H],
+ * X [T_k,D_KV], W_V [D_KV,H,D_H] -> O [T_q,H,D_H], lse [T_q,H] fp32
+ * log2-domain.  Each workgroup forms u = q_proj_h W_K,h^T for its rows on the
+ * matrix cores (fp32 accumulation, one rounding, as the reference's 16-bit
+ * GEMM), so u is never written to memory.  Shapes outside
+ * vafa_absorb_fold_supported return VAFA_ERR_VALUE; 16-byte aligned
+ * operands. */
+VAFA_API int vafa_absorb_fwd_fold(const void *q_proj, const void *W_K, const void *X,
+                                  const void *W_V, void *O, float *lse, const int32_t *plan_dev,
+                                  const vafa_plan_info *info, int64_t D_KV, int64_t D_H,
+                                  int32_t dtype, float scale, void *workspace,
+                                  int64_t workspace_bytes, void *stream);
+
 /* The head projection of packed_target_attn, which the reference runs as a
  * torch einsum (ta/interface.py:434-435, 'thd,khd->thk'):
  * u[t,h,f] = sum_d q_proj[t, h*D_H + d] * W_K[f,h,d] with q_proj [T_q, H*D_H],
@@ -246,8 +280,9 @@ VAFA_API int64_t vafa_absorb_project_workspace(int64_t T_q, int64_t H, int64_t D
  * q_proj [T_q, H*D_H] = q_raw [T_q, D_Q] . W_Q [D_Q, H*D_H] and
  * u [T_q, H, D_KV] = per head q_proj W_K[:,h,:]^T, each rounded once to the
  * 16-bit dtype (as the reference's two 16-bit GEMMs).  q_proj is written for
- * the backward.  D_Q, D_KV, D_H positive multiples of 8, 16-byte aligned
- * operands and workspace. */
+ * the backward.  u may be NULL: then only q_proj is formed (the input of
+ * vafa_absorb_fwd_fold).  D_Q, D_KV, D_H positive multiples of 8, 16-byte
+ * aligned operands and workspace. */
 VAFA_API int vafa_absorb_project_fwd(const void *q_raw, const void *W_Q, const void *W_K,
                                      void *q_proj, void *u, int64_t T_q, int64_t H, int64_t D_Q,
                                      int64_t D_KV, int64_t D_H, int32_t dtype, void *workspace,

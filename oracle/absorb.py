@@ -79,8 +79,21 @@ def forward(u, X, W_V, cu_q, cu_k, scale, dtype=np.float32, return_ax=False):
     return O, lse
 
 
-def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
-    """Inner op backward: returns ``(du, dX, dW_V)``."""
+def _ident(x):
+    return x
+
+
+def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32, round_to=None):
+    """Inner op backward: returns ``(du, dX, dW_V)``.
+
+    ``round_to`` (a function of an array, e.g. rounding to bf16) applies the
+    reference kernels' rounding points: delta = rowsum(O * dO) from O as
+    stored in the input dtype (ta/kernels.py:298-325 reads the forward's
+    output), dAX = dO W_V^T before the products it feeds (ta/kernels.py:480,
+    and the dX kernels), P and dS before the products with X and u (484-486),
+    aX before dW_V = aX^T dO (491), and du on its store (498).  With None
+    every step is exact in ``dtype``."""
+    r = _ident if round_to is None else (lambda a: np.asarray(round_to(a), dtype=dtype))
     u = np.asarray(u, dtype=dtype)
     X = np.asarray(X, dtype=dtype)
     W_V = np.asarray(W_V, dtype=dtype)
@@ -93,6 +106,7 @@ def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
     dax_all = np.empty_like(u)                                   # dO W_V^T per head
     for h in range(H):
         dax_all[:, h, :] = dO[:, h, :] @ W_V[:, h, :].T
+    dax_all = r(dax_all)
     for q0, q1, k0, k1 in _segs(cu_q, cu_k):
         if q1 == q0 or k1 == k0:
             continue
@@ -103,15 +117,22 @@ def backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)                       # [Lq*H, Lk]
-        ax_all[q0:q1] = (p @ xs).reshape(q1 - q0, H, D_KV)
         dp = dax @ xs.T
-        ds = p * (dp - (p * dp).sum(axis=-1, keepdims=True))
+        if round_to is None:
+            delta = (p * dp).sum(axis=-1, keepdims=True)
+        else:  # O = (P X) W_V per head, rounded, dotted with dO
+            o_r = r(_per_head((p @ xs).reshape(q1 - q0, H, D_KV), W_V))
+            delta = (o_r * dO[q0:q1]).sum(axis=-1).reshape(-1, 1)
+        ds = r(p * (dp - delta))
+        p = r(p)
+        ax_all[q0:q1] = (p @ xs).reshape(q1 - q0, H, D_KV)
         du[q0:q1] = ((ds @ xs) * sc).reshape(q1 - q0, H, D_KV)
         dX[k0:k1] = (ds.T @ u2) * sc + p.T @ dax
+    ax_all = r(ax_all)
     dW_V = np.empty_like(W_V)
     for h in range(H):
         dW_V[:, h, :] = ax_all[:, h, :].T @ dO[:, h, :]
-    return du, dX, dW_V
+    return r(du), dX, dW_V
 
 
 def full_forward(q_raw, X, W_Q, W_K, W_V, cu_q, cu_k, scale, dtype=np.float32):
@@ -120,21 +141,25 @@ def full_forward(q_raw, X, W_Q, W_K, W_V, cu_q, cu_k, scale, dtype=np.float32):
     return forward(u, X, W_V, cu_q, cu_k, scale, dtype)[0]
 
 
-def full_backward(q_raw, X, W_Q, W_K, W_V, dO, cu_q, cu_k, scale, dtype=np.float32):
+def full_backward(q_raw, X, W_Q, W_K, W_V, dO, cu_q, cu_k, scale, dtype=np.float32,
+                  round_to=None):
     """Grads of ``packed_target_attn`` w.r.t. (q_raw, X, W_Q, W_K, W_V).
 
     The u-projection gradients follow the chain rule through
-    ta/interface.py:434-435.
-    """
+    ta/interface.py:434-435.  ``round_to`` applies, besides the inner
+    backward's rounding points, those of the reference's 16-bit torch
+    products: q_proj and u in the forward, dq_proj = du W_K before the
+    products it feeds (dq_raw, dW_Q)."""
+    r = _ident if round_to is None else (lambda a: np.asarray(round_to(a), dtype=dtype))
     q_raw = np.asarray(q_raw, dtype=dtype)
     W_Q = np.asarray(W_Q, dtype=dtype)
     W_K = np.asarray(W_K, dtype=dtype)
     T, d_q = q_raw.shape
     _, H, D_H = W_Q.shape
-    qp = (q_raw @ W_Q.reshape(d_q, H * D_H)).reshape(T, H, D_H)
-    u = np.einsum("thd,khd->thk", qp, W_K)
-    du, dX, dW_V = backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype)
-    dqp = np.einsum("thk,khd->thd", du, W_K)
+    qp = r((q_raw @ W_Q.reshape(d_q, H * D_H)).reshape(T, H, D_H))
+    u = r(np.einsum("thd,khd->thk", qp, W_K))
+    du, dX, dW_V = backward(u, X, W_V, dO, cu_q, cu_k, scale, dtype, round_to=round_to)
+    dqp = r(np.einsum("thk,khd->thd", du, W_K))
     dW_K = np.einsum("thk,thd->khd", du, qp)
     dq_raw = dqp.reshape(T, H * D_H) @ W_Q.reshape(d_q, H * D_H).T
     dW_Q = (q_raw.T @ dqp.reshape(T, H * D_H)).reshape(d_q, H, D_H)

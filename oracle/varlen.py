@@ -54,8 +54,15 @@ def forward(q, k, v, cu_q, cu_k, scale, dtype=np.float32):
     return o, lse
 
 
-def backward(q, k, v, do, cu_q, cu_k, scale, dtype=np.float32):
-    """Returns ``(dq, dk, dv)`` (same shapes as q, k, v) in ``dtype``."""
+def backward(q, k, v, do, cu_q, cu_k, scale, dtype=np.float32, round_ps=None):
+    """Returns ``(dq, dk, dv)`` (same shapes as q, k, v) in ``dtype``.
+
+    ``round_ps`` (a function of an array, e.g. rounding to bf16) applies the
+    reference kernels' rounding points: delta = rowsum(O * dO) is formed from
+    O as stored in the input dtype (fa/kernels.py:186-216 reads the forward's
+    output), P is rounded before dV = P^T dO and dS before dQ = dS K and
+    dK = dS^T Q (fa/kernels.py:345, 480, 489).  With None every step is exact
+    in ``dtype``."""
     q = np.asarray(q, dtype=dtype)
     k = np.asarray(k, dtype=dtype)
     v = np.asarray(v, dtype=dtype)
@@ -77,8 +84,15 @@ def backward(q, k, v, do, cu_q, cu_k, scale, dtype=np.float32):
         p /= p.sum(axis=-1, keepdims=True)
         dvh = np.matmul(p.transpose(0, 2, 1), doh)              # [H, Lk, D]
         dp = np.matmul(doh, vh.transpose(0, 2, 1))              # [H, Lq, Lk]
-        delta = (p * dp).sum(axis=-1, keepdims=True)
+        if round_ps is None:
+            delta = (p * dp).sum(axis=-1, keepdims=True)
+        else:
+            o_r = np.asarray(round_ps(np.matmul(p, vh)), dtype=dtype)      # [H, Lq, D]
+            delta = (o_r * doh).sum(axis=-1, keepdims=True)
         ds = p * (dp - delta)
+        if round_ps is not None:
+            dvh = np.matmul(np.asarray(round_ps(p), dtype=dtype).transpose(0, 2, 1), doh)
+            ds = np.asarray(round_ps(ds), dtype=dtype)
         dq[q0:q1] = (np.matmul(ds, kh) * sc).transpose(1, 0, 2)
         dk[k0:k1] = (np.matmul(ds.transpose(0, 2, 1), qh) * sc).transpose(1, 0, 2)
         dv[k0:k1] = dvh.transpose(1, 0, 2)

@@ -395,3 +395,87 @@ def test_project_rejects_bad_shapes(device):
                                    x.data_ptr(), 1, 1, 8, 8, 8, _lib.dtype_code(torch.float32),
                                    x.data_ptr(), 256, _lib.stream_ptr(device))
     assert rc != 0 and "16-bit" in _lib.last_error()
+
+
+# Folded projection (vafa_absorb_fwd_fold): packed_target_attn on 16-bit
+# matrix-core shapes forms u inside the attention kernel.  Shapes: the
+# benchmark one, one head per wave (H <= 4), D_H = 16 (half the k slots of
+# the u product are zero), D_H = 64 / 128 (two / four 32-wide k steps), and
+# feature widths that pad (216 -> 224, 192).
+FOLD_SHAPES = [(8, 32, 256), (1, 32, 64), (4, 16, 256), (2, 64, 128), (4, 128, 192),
+               (8, 64, 216)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("H,D_H,d_kv", FOLD_SHAPES, ids=[f"H{h}_DH{d}_F{f}" for h, d, f in FOLD_SHAPES])
+def test_absorb_fold_matches_unfused_and_oracle(device, H, D_H, d_kv, dtype):
+    """The folded forward and its backward against the fp64 oracle, and
+    against the unfused path (projection kernel writes u, then
+    target_attn_inner) within the same bound.  Lengths hold an empty query
+    segment, a split key range (9000 keys) and multi-workgroup samples."""
+    from varlenabsorbflashattn_amd.absorb import _fold_native, _project_u
+    q_lens, k_lens = [1, 9, 70, 0, 3, 16], [40, 300, 129, 5, 2500, 9000]
+    print(f"[absorb fold {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
+    ins = [t.to(dtype) for t in make_inputs(q_lens, k_lens, d_q=96, d_kv=d_kv, H=H, D_H=D_H)]
+    cq, ck = cu_from_lens(q_lens), cu_from_lens(k_lens)
+    dev = [t.to(device).requires_grad_(True) for t in ins]
+    assert _fold_native(*dev)
+    O = packed_target_attn(*dev, cu_seqlens_q=cq.to(device), cu_seqlens_k=ck.to(device))
+    g = torch.Generator().manual_seed(7)
+    dO = (torch.randn(O.shape, generator=g) * 0.1).to(dtype)
+    O.backward(dO.to(device))
+    dev2 = [t.to(device).requires_grad_(True) for t in ins]
+    u = _project_u(dev2[0], dev2[2], dev2[3])
+    O2 = target_attn_inner(u, dev2[1], dev2[4], cq.to(device), ck.to(device))
+    O2.backward(dO.to(device))
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(D_H)
+    npy = [t.float().numpy() for t in ins]
+    O_ref = oa.full_forward(*npy, cq.numpy(), ck.numpy(), scale, np.float64)
+    grads = oa.full_backward(*npy, dO.float().numpy(), cq.numpy(), ck.numpy(), scale, np.float64)
+    for n, a, b, r in zip(NAMES, [O] + [t.grad for t in dev], [O2] + [t.grad for t in dev2],
+                          [O_ref] + list(grads)):
+        assert_close(n, a, r)
+        assert_close(n + " vs unfused", a, b.detach().float().cpu().numpy())
+
+
+def test_absorb_fold_negative_scale(device):
+    """A negative scale is folded into u as an exact sign flip (before the
+    rounding) by the folded kernel, as by the u-reading one."""
+    q_lens, k_lens = [3, 8, 1], [50, 700, 3000]
+    ins = [t.to(torch.bfloat16) for t in make_inputs(q_lens, k_lens, d_q=64, d_kv=256)]
+    cq, ck = cu_from_lens(q_lens), cu_from_lens(k_lens)
+    O = packed_target_attn(*(t.to(device) for t in ins), cu_seqlens_q=cq.to(device),
+                           cu_seqlens_k=ck.to(device), scale=-0.3)
+    npy = [t.float().numpy() for t in ins]
+    O_ref = oa.full_forward(*npy, cq.numpy(), ck.numpy(), -0.3, np.float64)
+    assert_close("O", O, O_ref)
+
+
+def test_absorb_fold_prepared_indices_issue_no_device_sync(device):
+    """The folded packed_target_attn keeps the prepare_target_attn_indices +
+    validate=False contract: forward + backward make no synchronizing call
+    and give the validated call's results bit for bit."""
+    from varlenabsorbflashattn_amd.absorb import _fold_native
+    q_lens, k_lens = [7, 8, 6, 9], [2048, 1024, 1536, 512]
+    ins = [t.to(device, torch.bfloat16) for t in make_inputs(q_lens, k_lens)]
+    assert _fold_native(*ins)
+    cq, ck = cu_from_lens(q_lens).to(device), cu_from_lens(k_lens).to(device)
+    qi, ki = prepare_target_attn_indices(cq, ck)
+
+    def run(**kw):
+        xs = [t.detach().clone().requires_grad_(True) for t in ins]
+        o = packed_target_attn(*xs, cu_seqlens_q=cq, cu_seqlens_k=ck, **kw)
+        o.backward(torch.ones_like(o))
+        return [o.detach()] + [t.grad for t in xs]
+
+    ref = run()
+    run(q_chunk_indices=qi, k_chunk_indices=ki, validate=False)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        got = run(q_chunk_indices=qi, k_chunk_indices=ki, validate=False)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)

@@ -4,14 +4,15 @@ Every configuration that bench.py times is checked here on its own shape and
 plan, against the numpy oracle in float32 on the host (the north-star
 reference precision) with the tolerances of tests/parity.py:
   * configs[1] (C2): the whole 64-sequence H=16 D=128 batch, O and all grads;
-  * configs[2] (C3): a seeded 24-sequence subset at H=32 D=128 that holds the
-    longest key range and both extreme query lengths, plus the 4-16 key chunks
-    per (sequence, head) that the config prescribes;
+  * configs[2] (C3): the full 256-sequence launch that bench.py times (its
+    own plan, 4-16 key chunks per (sequence, head)), every head compared in
+    groups of four; plus a seeded 24-sequence subset with its plan asserted;
   * configs[3] (C4): all 2048 samples, inner forward and backward;
-  * configs[4] (C5): the full 8192-sample forward (its own plan), with the
-    output rows of 256 samples -- every sample at the 8192-key cap with the
-    most queries among them -- compared against the oracle.
+  * configs[4] (C5): the full 8192-sample forward (its own plan), every
+    sample's output rows compared against the oracle in batches.
 Inputs follow varlenabsorbflashattn_amd.workloads (the generator bench.py uses).
+Bounds: tests/parity.py (raw max-abs <= 2e-2 on tensors with max |ref| <= 2,
+raw mean-abs <= 2e-3 up to max |ref| = 4).
 """
 import math
 
@@ -21,7 +22,7 @@ import torch
 
 from oracle import absorb as oa
 from oracle import varlen as ov
-from parity import assert_close
+from parity import assert_close, assert_within_reference_numerics
 from varlenabsorbflashattn_amd import (_lib, packed_varlen_attn, prepare_target_attn_indices,
                                        target_attn_inner)
 from varlenabsorbflashattn_amd import workloads as W
@@ -99,6 +100,35 @@ def test_c3_subset_split_forward(device):
     assert_close("o", o, o_r)
 
 
+def test_c3_full_size_split_forward(device):
+    """The whole C3 launch (256 sequences, H=32, D=128, every tile split into
+    4-16 key chunks and merged by the LSE combine), compared head group by
+    head group against the fp32 oracle: all 2,234 query rows x 32 heads."""
+    case = W.config3(seed=0)
+    lq, lk = np.asarray(case.q_lens), np.asarray(case.k_lens)
+    print(f"[C3 full] H={case.H} D={case.D} n={len(lq)} sum_Lq={int(lq.sum())} "
+          f"sum_Lk={int(lk.sum())} max_Lk={int(lk.max())}", flush=True)
+    plan = _lib.plan_varlen(_cu_np(case.q_lens), _cu_np(case.k_lens), case.H, case.D)
+    fwd = plan.section("fwd")
+    assert np.all(fwd[:, 4] >= 0) and fwd[:, 7].min() >= 4 and fwd[:, 7].max() <= 16
+    q, k, v = W.varlen_tensors(case, device)
+    cq, ck = W.cu_from_lens(case.q_lens, device), W.cu_from_lens(case.k_lens, device)
+    with torch.no_grad():
+        o = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(case.D)
+    cq_h, ck_h = _cu_np(case.q_lens), _cu_np(case.k_lens)
+    worst = dict(max_abs=0.0, mean_abs=0.0)
+    for h0 in range(0, case.H, 4):
+        hs = slice(h0, h0 + 4)
+        o_r, _ = ov.forward(_host(q[:, hs]), _host(k[:, hs]), _host(v[:, hs]), cq_h, ck_h,
+                            scale, np.float32)
+        e = assert_close(f"o h{h0}-{h0 + 3}", o[:, hs], o_r)
+        worst = {n: max(worst[n], e[n]) for n in worst}
+    print(f"  C3 all heads: max_abs={worst['max_abs']:.3e} "
+          f"max of group mean_abs={worst['mean_abs']:.3e}", flush=True)
+
+
 def _absorb_inputs(case, device, dtype=None):
     q_raw, X, W_Q, W_K, W_V = W.absorb_tensors(case, device, dtype=dtype)
     with torch.no_grad():
@@ -135,14 +165,52 @@ def test_c4_full_fwd_bwd(device, dtype):
         assert_close(n, a, r)
 
 
-def test_c5_full_plan_forward(device):
+def test_c4_whole_op_folded(device):
+    """configs[3] through packed_target_attn as bench.py times it: 16-bit
+    inputs take the folded projection (u formed inside the attention kernel),
+    forward and the five gradients against the fp32 oracle."""
+    from varlenabsorbflashattn_amd import packed_target_attn
+    from varlenabsorbflashattn_amd.absorb import _fold_native
+    case = W.config4(seed=0)
+    ins = W.absorb_tensors(case, device)
+    assert _fold_native(*ins)
+    print(f"[C4 whole op, folded] samples={len(case.q_lens)} T_q={sum(case.q_lens)} "
+          f"T_k={sum(case.k_lens)}", flush=True)
+    cq, ck = W.cu_from_lens(case.q_lens, device), W.cu_from_lens(case.k_lens, device)
+    dev = [t.detach().clone().requires_grad_(True) for t in ins]
+    O = packed_target_attn(*dev, cu_seqlens_q=cq, cu_seqlens_k=ck)
+    g = torch.Generator(device=device).manual_seed(11)
+    dO = torch.randn(O.shape, generator=g, device=device).to(O.dtype)
+    O.backward(dO)
+    torch.cuda.synchronize()
+    host = [_host(t) for t in ins]
+    cq_h, ck_h = _cu_np(case.q_lens), _cu_np(case.k_lens)
+    scale = 1.0 / math.sqrt(case.D_H)
+    O_r = oa.full_forward(*host, cq_h, ck_h, scale, np.float32)
+    grads = oa.full_backward(*host, _host(dO), cq_h, ck_h, scale, np.float32)
+    assert_close("O", O, O_r)
+    for n, a, r in zip(("dq_raw", "dX"), (dev[0].grad, dev[1].grad), grads[:2]):
+        assert_close(n, a, r)
+    # The weight gradients sum bf16 products over all 9,424 tokens: the
+    # reference's own roundings (du, dq_proj, P, dS, aX to bf16) put them at
+    # 2.9-3.4e-3 of rms(ref) in mean error, above the 2e-3 bound, so they
+    # are held to that envelope (oracle with the reference's rounding points)
+    bf16 = lambda x: torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)) \
+        .to(torch.bfloat16).float().numpy()
+    emul = oa.full_backward(*host, _host(dO), cq_h, ck_h, scale, np.float32, round_to=bf16)
+    for n, a, r, m in zip(("dW_Q", "dW_K", "dW_V"), (dev[2].grad, dev[3].grad, dev[4].grad),
+                          grads[2:], emul[2:]):
+        assert_within_reference_numerics(n, a, r, m)
+
+
+def test_c5_full_forward(device):
+    """The whole C5 forward (8192 samples on its own plan); every sample's
+    output rows are compared against the fp32 oracle, 1024 samples at a time
+    (X rows of a batch moved to the host per batch)."""
     case = W.config5(seed=0)
     lq, lk = np.asarray(case.q_lens), np.asarray(case.k_lens)
-    capped = np.flatnonzero(lk == lk.max())
-    capped = capped[np.argsort(-lq[capped], kind="stable")][:56]
-    pick = np.unique(np.concatenate([np.arange(200), capped]))
-    print(f"[C5 full] samples={len(lq)} T_q={int(lq.sum())} T_k={int(lk.sum())}; "
-          f"checking {len(pick)} samples ({len(capped)} at Lk={int(lk.max())})", flush=True)
+    print(f"[C5 full] samples={len(lq)} T_q={int(lq.sum())} T_k={int(lk.sum())} "
+          f"max_Lk={int(lk.max())}", flush=True)
     u, X, W_V = _absorb_inputs(case, device)
     cq, ck = W.cu_from_lens(case.q_lens, device), W.cu_from_lens(case.k_lens, device)
     qi, ki = prepare_target_attn_indices(cq, ck)
@@ -151,9 +219,17 @@ def test_c5_full_plan_forward(device):
         O = target_attn_inner(u, X, W_V, cq, ck, scale, qi, ki, validate=False)
     torch.cuda.synchronize()
     cq_h, ck_h = _cu_np(case.q_lens), _cu_np(case.k_lens)
-    q_rows = np.concatenate([np.arange(cq_h[i], cq_h[i + 1]) for i in pick])
-    k_rows = np.concatenate([np.arange(ck_h[i], ck_h[i + 1]) for i in pick])
-    qr, kr = torch.from_numpy(q_rows).to(device), torch.from_numpy(k_rows).to(device)
-    O_r, _ = oa.forward(_host(u[qr]), _host(X[kr]), _host(W_V), _cu_np(lq[pick]),
-                        _cu_np(lk[pick]), scale, np.float32)
-    assert_close("O", O[qr], O_r)
+    hW = _host(W_V)
+    sq, sd = 0.0, 0.0
+    worst = dict(max_abs=0.0, excess=0.0, ref_max=0.0)
+    for b0 in range(0, len(lq), 1024):
+        b1 = min(b0 + 1024, len(lq))
+        qs, qe, ks, ke = int(cq_h[b0]), int(cq_h[b1]), int(ck_h[b0]), int(ck_h[b1])
+        O_r, _ = oa.forward(_host(u[qs:qe]), _host(X[ks:ke]), hW, cq_h[b0:b1 + 1] - qs,
+                            ck_h[b0:b1 + 1] - ks, scale, np.float32)
+        e = assert_close(f"O {b0}-{b1 - 1}", O[qs:qe], O_r)
+        n = O_r.size
+        sq, sd = sq + n, sd + e["mean_abs"] * n
+        worst = {k_: max(worst[k_], e[k_]) for k_ in worst}
+    print(f"  C5 all samples: max_abs={worst['max_abs']:.3e} mean_abs={sd / sq:.3e} "
+          f"max_excess={worst['excess']:.3e} max|ref|={worst['ref_max']:.3e}", flush=True)

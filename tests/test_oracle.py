@@ -154,12 +154,150 @@ def test_backward_finite_differences():
             assert abs((lp - lm) / (2 * eps) - grad[idx]) < 1e-6
 
 
+def _brute_backward_rounded(q, k, v, do, lq, lk, sc, r):
+    """Scalar loops over one head: softmax attention backward with the
+    rounding ``r`` applied to each P and dS element before the products that
+    consume them (dV = r(P)^T dO, dQ = sc r(dS) K, dK = sc r(dS)^T Q) and to
+    O before delta = O . dO."""
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    q0 = k0 = 0
+    D = q.shape[-1]
+    for a, b in zip(lq, lk):
+        for h in range(q.shape[1]):
+            for i in range(q0, q0 + a):
+                s = [sc * sum(q[i, h, d] * k[j, h, d] for d in range(D)) for j in range(k0, k0 + b)]
+                m = max(s)
+                e = [math.exp(x - m) for x in s]
+                p = [x / sum(e) for x in e]
+                dp = [sum(do[i, h, d] * v[j, h, d] for d in range(D)) for j in range(k0, k0 + b)]
+                o = [r(sum(pp * v[j, h, d] for pp, j in zip(p, range(k0, k0 + b))))
+                     for d in range(D)]
+                delta = sum(o[d] * do[i, h, d] for d in range(D))
+                for jj, j in enumerate(range(k0, k0 + b)):
+                    ds = r(p[jj] * (dp[jj] - delta))
+                    for d in range(D):
+                        dv[j, h, d] += r(p[jj]) * do[i, h, d]
+                        dq[i, h, d] += sc * ds * k[j, h, d]
+                        dk[j, h, d] += sc * ds * q[i, h, d]
+        q0 += a
+        k0 += b
+    return dq, dk, dv
+
+
+def test_backward_reference_rounding_points():
+    """round_ps applies the reference kernels' roundings of P (before dV) and
+    dS (before dQ and dK): pinned against scalar loops with a coarse rounding
+    (two decimals, so a rounding applied to the wrong product or missing
+    shows), the identity rounding reproduces the exact backward (to the
+    summation order of delta = O . dO against sum_j P dP), and every gradient
+    moves under the coarse rounding."""
+    rng = np.random.default_rng(8)
+    lq, lk, H, D, sc = [3, 2, 0], [4, 3, 2], 2, 3, 0.9
+    q, k, v = _rand(rng, 5, H, D), _rand(rng, 9, H, D), _rand(rng, 9, H, D)
+    do = _rand(rng, 5, H, D)
+    coarse = lambda x: np.round(x, 2)
+    got = ov.backward(q, k, v, do, _cu(lq), _cu(lk), sc, np.float64, round_ps=coarse)
+    want = _brute_backward_rounded(q, k, v, do, lq, lk, sc, lambda x: round(x, 2))
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, atol=1e-12)
+    exact = ov.backward(q, k, v, do, _cu(lq), _cu(lk), sc, np.float64)
+    same = ov.backward(q, k, v, do, _cu(lq), _cu(lk), sc, np.float64, round_ps=lambda x: x)
+    for a, b, c in zip(exact, same, got):
+        np.testing.assert_allclose(a, b, atol=1e-12)  # delta summed in another order
+        assert np.abs(a - c).max() > 1e-4
+
+
 # ---- absorb ---------------------------------------------------------------------
 
 def _absorb_inputs(rng, lq, lk, d_q=12, d_kv=10, H=2, D_H=4):
     return (_rand(rng, sum(lq), d_q) * 0.5, _rand(rng, sum(lk), d_kv) * 0.5,
             _rand(rng, d_q, H, D_H) * 0.5, _rand(rng, d_kv, H, D_H) * 0.5,
             _rand(rng, d_kv, H, D_H) * 0.5)
+
+
+def _brute_absorb_backward_rounded(q_raw, X, W_Q, W_K, W_V, dO, lq, lk, sc, r):
+    """Scalar loops: grads of the absorbed op with the rounding ``r`` at each
+    rounding point the reference's kernels and 16-bit products have (q_proj,
+    u, dAX, P, dS, aX, du, dq_proj, and O before delta = O . dO)."""
+    T, d_q = q_raw.shape
+    F, H, DH = W_K.shape
+    qp = np.zeros((T, H, DH))
+    u = np.zeros((T, H, F))
+    for t in range(T):
+        for h in range(H):
+            for d in range(DH):
+                qp[t, h, d] = r(sum(q_raw[t, c] * W_Q[c, h, d] for c in range(d_q)))
+            for f in range(F):
+                u[t, h, f] = r(sum(qp[t, h, d] * W_K[f, h, d] for d in range(DH)))
+    du, dX, ax = np.zeros_like(u), np.zeros_like(X), np.zeros_like(u)
+    dax = np.zeros_like(u)
+    for t in range(T):
+        for h in range(H):
+            for f in range(F):
+                dax[t, h, f] = r(sum(dO[t, h, d] * W_V[f, h, d] for d in range(DH)))
+    q0 = k0 = 0
+    for a, b in zip(lq, lk):
+        for t in range(q0, q0 + a):
+            for h in range(H):
+                s = [sc * sum(u[t, h, f] * X[j, f] for f in range(F)) for j in range(k0, k0 + b)]
+                m = max(s)
+                e = [math.exp(x - m) for x in s]
+                p = [x / sum(e) for x in e]
+                dp = [sum(dax[t, h, f] * X[j, f] for f in range(F)) for j in range(k0, k0 + b)]
+                axr = [sum(pp * X[j, f] for pp, j in zip(p, range(k0, k0 + b))) for f in range(F)]
+                o = [r(sum(axr[f] * W_V[f, h, d] for f in range(F))) for d in range(DH)]
+                delta = sum(o[d] * dO[t, h, d] for d in range(DH))
+                for jj, j in enumerate(range(k0, k0 + b)):
+                    ds, pr = r(p[jj] * (dp[jj] - delta)), r(p[jj])
+                    for f in range(F):
+                        ax[t, h, f] += pr * X[j, f]
+                        du[t, h, f] += sc * ds * X[j, f]
+                        dX[j, f] += sc * ds * u[t, h, f] + pr * dax[t, h, f]
+        q0 += a
+        k0 += b
+    dW_V = np.zeros_like(W_V)
+    dqp, dW_K, dW_Q, dq = np.zeros_like(qp), np.zeros_like(W_K), np.zeros_like(W_Q), np.zeros_like(q_raw)
+    for t in range(T):
+        for h in range(H):
+            for f in range(F):
+                du[t, h, f] = r(du[t, h, f])
+                for d in range(DH):
+                    dW_V[f, h, d] += r(ax[t, h, f]) * dO[t, h, d]
+            for d in range(DH):
+                dqp[t, h, d] = r(sum(du[t, h, f] * W_K[f, h, d] for f in range(F)))
+    for t in range(T):
+        for h in range(H):
+            for d in range(DH):
+                for f in range(F):
+                    dW_K[f, h, d] += du[t, h, f] * qp[t, h, d]
+                for c in range(d_q):
+                    dW_Q[c, h, d] += q_raw[t, c] * dqp[t, h, d]
+                    dq[t, c] += dqp[t, h, d] * W_Q[c, h, d]
+    return dq, dX, dW_Q, dW_K, dW_V
+
+
+def test_absorb_backward_reference_rounding_points():
+    """full_backward(round_to=...) applies the reference's rounding points:
+    pinned against scalar loops with a coarse rounding (two decimals, so a
+    rounding missing or applied to the wrong operand shows); the identity
+    rounding reproduces the exact gradients (to the summation order of delta
+    = O . dO against sum_j P dP), and every gradient moves under the coarse
+    rounding."""
+    rng = np.random.default_rng(9)
+    lq, lk = [2, 1, 0], [3, 2, 4]
+    ins = _absorb_inputs(rng, lq, lk, d_q=3, d_kv=3, H=2, D_H=2)
+    ins = tuple(x * 3 for x in ins)
+    dO = _rand(rng, sum(lq), 2, 2)
+    sc, cu_q, cu_k = 0.8, _cu(lq), _cu(lk)
+    got = oa.full_backward(*ins, dO, cu_q, cu_k, sc, np.float64, round_to=lambda x: np.round(x, 2))
+    want = _brute_absorb_backward_rounded(*ins, dO, lq, lk, sc, lambda x: round(x, 2))
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, atol=1e-10)
+    exact = oa.full_backward(*ins, dO, cu_q, cu_k, sc, np.float64)
+    same = oa.full_backward(*ins, dO, cu_q, cu_k, sc, np.float64, round_to=lambda x: x)
+    for a, b, c in zip(exact, same, got):
+        np.testing.assert_allclose(a, b, atol=1e-12)
+        assert np.abs(a - c).max() > 1e-4
 
 
 def test_absorbed_equals_explicit():

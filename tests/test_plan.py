@@ -115,10 +115,49 @@ def test_validate_cu_absorb_texts(cu, T, fa_text, ta_text):
     assert _outcome(_lib.validate_cu_absorb, cu, T) == ta_text
 
 
-def test_active_segments_have_keys():
-    _lib.check_active_have_keys(np.array([0, 2, 2]), np.array([0, 5, 5]))
-    with pytest.raises(ValueError, match="k_len > 0"):
-        _lib.check_active_have_keys(np.array([0, 2, 3]), np.array([0, 5, 5]))
+ACTIVE_TEXT = "segments with q_len > 0 must have k_len > 0"  # ta/interface.py:116
+
+ACTIVE_CASES = [
+    # (cu_q, cu_k, raises): literal cases of ta/interface.py:109-116
+    ([0, 2, 2], [0, 5, 5], False),     # a trailing segment with no queries and no keys
+    ([0, 2, 3], [0, 5, 5], True),      # 1 query against 0 keys
+    ([0, 0, 3], [0, 0, 4], False),     # empty first segment on both sides
+    ([0, 0], [0, 7], False),           # keys without queries
+    ([0, 4], [0, 0], True),            # the only segment has queries and no keys
+    ([0], [0], False),                 # no segments at all
+    ([0, 1, 1, 2], [0, 3, 3, 3], True),  # the last segment alone violates it
+]
+
+
+def _active_outcome(fn, cq, ck):
+    try:
+        fn(np.array(cq), np.array(ck))
+        return None
+    except ValueError as e:
+        return str(e)
+
+
+@pytest.mark.parametrize("cq,ck,raises", ACTIVE_CASES)
+def test_active_segments_have_keys(cq, ck, raises):
+    """Oracle (oracle/meta.py) and product (vafa_check_active_have_keys) give
+    the reference's outcome and exact text on literal cases."""
+    want = ACTIVE_TEXT if raises else None
+    assert _active_outcome(meta.active_segments_have_keys, cq, ck) == want
+    assert _active_outcome(_lib.check_active_have_keys, cq, ck) == want
+
+
+def test_active_segments_have_keys_brute_force():
+    """Random segment tables with zero lengths on either side: the oracle and
+    the product agree with a per-segment loop over the rule."""
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        n = int(rng.integers(1, 12))
+        lq = rng.integers(0, 3, size=n) * rng.integers(0, 2, size=n)
+        lk = rng.integers(0, 3, size=n) * rng.integers(0, 2, size=n)
+        bad = any(a > 0 and b == 0 for a, b in zip(lq.tolist(), lk.tolist()))
+        want = ACTIVE_TEXT if bad else None
+        assert _active_outcome(meta.active_segments_have_keys, _cu(lq), _cu(lk)) == want
+        assert _active_outcome(_lib.check_active_have_keys, _cu(lq), _cu(lk)) == want
 
 
 @pytest.mark.parametrize("bt", [16, 64, 128])
@@ -454,3 +493,27 @@ def test_varlen_entry_rejects_plan_of_another_head_dim():
     assert rc != 0 and "head_dim 256" in _lib.last_error()
     with pytest.raises(ValueError, match="build the plan with this head_dim"):
         _lib.check(rc)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_varlen_bwd_rejects_fused_items_at_wider_head_dim(D):
+    """A D=64 plan holds fused key-major items (chunks of up to 3 x 128 keys
+    for segments of <= 16 queries); the dK/dV kernels of D=128/256 cover one
+    key tile per item, so the C ABI refuses that plan at those head dims
+    before any device call (no pointer is dereferenced: all are null)."""
+    import ctypes as C
+    cq, ck = _cu([5, 100]), _cu([3000, 300])
+    p = _lib.plan_varlen(cq, ck, 2, 64)
+    assert p.info.n_fkv > 0 and (p.info.q_tile, p.info.k_tile) == (128, 128)
+    lib = _lib.lib()
+    for stage in (-1, 2):
+        if stage < 0:
+            rc = lib.vafa_varlen_bwd(None, None, None, None, None, None, None, None, None, None,
+                                     C.byref(p.info), D, _lib.DT_BF16, 0.1, None, 0, None)
+        else:
+            rc = lib.vafa_varlen_bwd_stage(stage, None, None, None, None, None, None, None,
+                                           None, None, None, C.byref(p.info), D, _lib.DT_BF16,
+                                           0.1, None, 0, None)
+        assert rc != 0 and "fused key-major items" in _lib.last_error()
+        with pytest.raises(ValueError, match="build the plan with this head_dim"):
+            _lib.check(rc)

@@ -66,6 +66,8 @@ _SIGS = {
     "vafa_varlen_bwd_workspace": (C.c_int64, [_PINFO, _I64]),
     "vafa_absorb_fwd_workspace": (C.c_int64, [_PINFO, _I64, _I64]),
     "vafa_absorb_bwd_workspace": (C.c_int64, [_PINFO, _I64, _I64]),
+    "vafa_absorb_fwd_fold_workspace": (C.c_int64, [_PINFO, _I64, _I64]),
+    "vafa_absorb_fold_supported": (C.c_int, [_I64, _I64, _I64, _I32]),
     "vafa_varlen_fwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _PINFO, _I64, _I32, C.c_float,
                                   _P, _I64, _P]),
     "vafa_varlen_fwd_noalloc": (C.c_int, [_P, _P, _P, _P, _P, _P, _PINFO, _I64, _I32, C.c_float,
@@ -84,6 +86,8 @@ _SIGS = {
                                   _P, _I64, _P]),
     "vafa_absorb_bwd": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _PINFO, _I64, _I64,
                                   _I32, C.c_float, _P, _I64, _P]),
+    "vafa_absorb_fwd_fold": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _PINFO, _I64, _I64, _I32,
+                                       C.c_float, _P, _I64, _P]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -1,10 +1,13 @@
 """Ragged absorbed target attention -- drop-in for
 ``triton_target_attn_absorb`` (ta/interface.py:125-454).
 
-``packed_target_attn`` keeps the reference signature: it projects
-``u = q_raw W_Q W_K^T`` per head with plain library GEMMs (autograd carries
-dq_raw / dW_Q / dW_K, as in ta/interface.py:429-435) and calls
-``target_attn_inner``, whose forward and backward run in ``libvafa.so``:
+``packed_target_attn`` keeps the reference signature.  For 16-bit inputs on
+the matrix-core shapes it forms ``q_proj = q_raw W_Q`` and runs the attention
+with ``u = q_proj W_K^T`` formed inside the attention kernel (u never reaches
+memory in the forward); otherwise it projects ``u`` per head (this library's
+projection kernels, or torch GEMMs for fp32 / odd widths, as in
+ta/interface.py:429-435) and calls ``target_attn_inner``, whose forward and
+backward run in ``libvafa.so``:
 scores are taken directly against the raw ``X`` rows, ``aX = softmax(u X^T) X``
 is accumulated on the fly and projected by ``W_V`` at the end.  The backward
 is deterministic (dW_V and dX are reduced in a fixed order).
@@ -131,6 +134,59 @@ def _aligned(x: torch.Tensor) -> torch.Tensor:
     return x.clone() if x.data_ptr() % 16 != 0 else x
 
 
+def _absorb_plan(T_q, T_k, H, D_KV, D_H, device, cu_seqlens_q, cu_seqlens_k,
+                 q_chunk_indices, validate):
+    """Validation (ta/interface.py:92-122, 176-201) and the cached device plan
+    of one absorb call; host cu_seqlens come from the prepared index tables
+    when they belong to these very tensors and validation is off."""
+    known = _recall_host_cu(q_chunk_indices, cu_seqlens_q, cu_seqlens_k)
+    if known is not None and not validate:
+        cu_q_h, cu_k_h = known
+    else:
+        cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
+    if validate:
+        n_seg = cu_seqlens_q.numel() - 1
+        assert cu_seqlens_k.numel() - 1 == n_seg, "segment count mismatch q vs k"
+        _validate_cu_seqlens(cu_q_h, cu_seqlens_q.shape, T_q, "cu_seqlens_q")
+        _validate_cu_seqlens(cu_k_h, cu_seqlens_k.shape, T_k, "cu_seqlens_k")
+        _lib.check_active_have_keys(cu_q_h, cu_k_h)
+    B_DKV = _next_power_of_2(D_KV)
+    assert B_DKV <= 512, f"D_KV={D_KV} pads to {B_DKV}, which is too large for v1 tiles"
+    plan = _lib.device_plan("absorb", cu_q_h, cu_k_h, (H, D_KV, D_H), device)
+    if plan.info.T_q > T_q or plan.info.T_k > T_k:
+        raise ValueError(
+            f"cu_seqlens address {plan.info.T_q} query / {plan.info.T_k} key tokens but "
+            f"the inputs hold {T_q} / {T_k}")
+    if plan.info.n_fwd > 0:
+        _select_fwd_mode()
+    return plan
+
+
+def _absorb_bwd(u, X, W_V, O, LSE, dO, plan, scale):
+    """du, dX, dW_V of the inner op through vafa_absorb_bwd."""
+    T_q, H, D_KV = u.shape
+    D_H = W_V.shape[2]
+    if dO.stride(-1) != 1 or not dO.is_contiguous():
+        dO = dO.contiguous()
+    if dO.dtype != u.dtype:
+        dO = dO.to(u.dtype)
+    dO = _aligned(dO)
+    if plan.info.n_kv > 0:
+        _select_dx_mode(int(plan.info.n_kv))
+    du = torch.empty_like(u)
+    dX = torch.empty_like(X)
+    dW_V = torch.empty_like(W_V)
+    L = _lib.lib()
+    ws = _workspace(L.vafa_absorb_bwd_workspace(plan.info, D_KV, D_H), u.device)
+    _lib.check(L.vafa_absorb_bwd(
+        u.data_ptr(), X.data_ptr(), W_V.data_ptr(), O.data_ptr(), dO.data_ptr(),
+        LSE.data_ptr(), du.data_ptr(), dX.data_ptr(), dW_V.data_ptr(),
+        plan.items.data_ptr(), plan.info, D_KV, D_H, _lib.dtype_code(u.dtype),
+        float(scale), ws.data_ptr() if ws.numel() else None, ws.numel(),
+        _lib.stream_ptr(u.device)))
+    return du, dX, dW_V
+
+
 class _TargetAttnFunction(torch.autograd.Function):
     """Inner op on projected u (ta/interface.py:141-321)."""
 
@@ -149,32 +205,11 @@ class _TargetAttnFunction(torch.autograd.Function):
         assert u.device == X.device == W_V.device, "u/X/W_V must be on same device"
         assert D_H in (16, 32, 64, 128, 256), f"D_H {D_H} not supported"
         dcode = _lib.dtype_code(u.dtype)
-
-        known = _recall_host_cu(q_chunk_indices, cu_seqlens_q, cu_seqlens_k)
-        if known is not None and not validate:
-            cu_q_h, cu_k_h = known
-        else:
-            cu_q_h, cu_k_h = _lib.as_host_i64_pair(cu_seqlens_q, cu_seqlens_k)
-        if validate:
-            n_seg = cu_seqlens_q.numel() - 1
-            assert cu_seqlens_k.numel() - 1 == n_seg, "segment count mismatch q vs k"
-            _validate_cu_seqlens(cu_q_h, cu_seqlens_q.shape, T_q, "cu_seqlens_q")
-            _validate_cu_seqlens(cu_k_h, cu_seqlens_k.shape, T_k, "cu_seqlens_k")
-            _lib.check_active_have_keys(cu_q_h, cu_k_h)
-
         u, X, W_V = (_aligned(t.contiguous()) for t in (u, X, W_V))
-        B_DKV = _next_power_of_2(D_KV)
-        assert B_DKV <= 512, f"D_KV={D_KV} pads to {B_DKV}, which is too large for v1 tiles"
-
-        plan = _lib.device_plan("absorb", cu_q_h, cu_k_h, (H, D_KV, D_H), u.device)
-        if plan.info.T_q > T_q or plan.info.T_k > T_k:
-            raise ValueError(
-                f"cu_seqlens address {plan.info.T_q} query / {plan.info.T_k} key tokens but "
-                f"the inputs hold {T_q} / {T_k}")
+        plan = _absorb_plan(T_q, T_k, H, D_KV, D_H, u.device, cu_seqlens_q, cu_seqlens_k,
+                            q_chunk_indices, validate)
         O = torch.empty((T_q, H, D_H), dtype=u.dtype, device=u.device)
         LSE = torch.empty((T_q, H), dtype=torch.float32, device=u.device)
-        if plan.info.n_fwd > 0:
-            _select_fwd_mode()
         L = _lib.lib()
         ws = _workspace(L.vafa_absorb_fwd_workspace(plan.info, D_KV, D_H), u.device)
         _lib.check(L.vafa_absorb_fwd(
@@ -189,27 +224,7 @@ class _TargetAttnFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dO):
         u, X, W_V, O, LSE = ctx.saved_tensors
-        plan = ctx.plan
-        T_q, H, D_KV = u.shape
-        D_H = W_V.shape[2]
-        if dO.stride(-1) != 1 or not dO.is_contiguous():
-            dO = dO.contiguous()
-        if dO.dtype != u.dtype:
-            dO = dO.to(u.dtype)
-        dO = _aligned(dO)
-        if plan.info.n_kv > 0:
-            _select_dx_mode(int(plan.info.n_kv))
-        du = torch.empty_like(u)
-        dX = torch.empty_like(X)
-        dW_V = torch.empty_like(W_V)
-        L = _lib.lib()
-        ws = _workspace(L.vafa_absorb_bwd_workspace(plan.info, D_KV, D_H), u.device)
-        _lib.check(L.vafa_absorb_bwd(
-            u.data_ptr(), X.data_ptr(), W_V.data_ptr(), O.data_ptr(), dO.data_ptr(),
-            LSE.data_ptr(), du.data_ptr(), dX.data_ptr(), dW_V.data_ptr(),
-            plan.items.data_ptr(), plan.info, D_KV, D_H, _lib.dtype_code(u.dtype),
-            float(ctx.scale), ws.data_ptr() if ws.numel() else None, ws.numel(),
-            _lib.stream_ptr(u.device)))
+        du, dX, dW_V = _absorb_bwd(u, X, W_V, O, LSE, dO, ctx.plan, ctx.scale)
         return du, dX, dW_V, None, None, None, None, None, None
 
 
@@ -294,6 +309,86 @@ class _Project(torch.autograd.Function):
         return dq, dwq, dwk
 
 
+def _fold_native(q_raw, X, W_Q, W_K, W_V) -> bool:
+    """Whether packed_target_attn can run with u folded into the attention
+    kernel (vafa_absorb_fwd_fold): the native projection's operands, X and
+    W_V of the same dtype on the same device, and a shape of the folded
+    matrix-core kernel."""
+    if not _project_native(q_raw, W_Q, W_K):
+        return False
+    if X.dtype != q_raw.dtype or W_V.dtype != q_raw.dtype or not (X.is_cuda and W_V.is_cuda):
+        return False
+    if not (q_raw.device == X.device == W_Q.device == W_K.device == W_V.device):
+        return False
+    d_kv, H, D_H = W_K.shape
+    return bool(_lib.lib().vafa_absorb_fold_supported(H, d_kv, D_H,
+                                                      _lib.dtype_code(q_raw.dtype)))
+
+
+class _FoldedTargetAttn(torch.autograd.Function):
+    """packed_target_attn with the u projection folded into the attention
+    forward (ta/interface.py:429-435 followed by ta/interface.py:141-321).
+
+    Forward: q_proj = q_raw W_Q (row-GEMM kernel, rounded to the input dtype),
+    then vafa_absorb_fwd_fold, whose workgroups form u = q_proj_h W_K,h^T for
+    their own rows on the matrix cores -- u is never written to memory.
+    Backward: u is formed once from the saved q_proj (vafa_absorb_project_u,
+    the same products), then the inner backward gives du / dX / dW_V and the
+    projection backward dq_raw / dW_Q / dW_K, as the unfused path."""
+
+    @staticmethod
+    def forward(ctx, q_raw, X, W_Q, W_K, W_V, cu_seqlens_q, cu_seqlens_k, scale,
+                q_chunk_indices, k_chunk_indices, validate):
+        T_q, d_q = q_raw.shape
+        T_k, d_kv = X.shape
+        _, H, D_H = W_Q.shape
+        dcode = _lib.dtype_code(q_raw.dtype)
+        q_raw, X, W_Q, W_K, W_V = (_aligned(t.contiguous()) for t in (q_raw, X, W_Q, W_K, W_V))
+        plan = _absorb_plan(T_q, T_k, H, d_kv, D_H, X.device, cu_seqlens_q, cu_seqlens_k,
+                            q_chunk_indices, validate)
+        L = _lib.lib()
+        st = _lib.stream_ptr(X.device)
+        q_proj = torch.empty((T_q, H * D_H), dtype=q_raw.dtype, device=q_raw.device)
+        pws = _workspace(L.vafa_absorb_project_workspace(T_q, H, d_q, d_kv, D_H, 0), X.device)
+        _lib.check(L.vafa_absorb_project_fwd(
+            q_raw.data_ptr(), W_Q.data_ptr(), W_K.data_ptr(), q_proj.data_ptr(), None,
+            T_q, H, d_q, d_kv, D_H, dcode, pws.data_ptr(), pws.numel(), st))
+        O = torch.empty((T_q, H, D_H), dtype=q_raw.dtype, device=X.device)
+        LSE = torch.empty((T_q, H), dtype=torch.float32, device=X.device)
+        ws = _workspace(L.vafa_absorb_fwd_fold_workspace(plan.info, d_kv, D_H), X.device)
+        _lib.check(L.vafa_absorb_fwd_fold(
+            q_proj.data_ptr(), W_K.data_ptr(), X.data_ptr(), W_V.data_ptr(), O.data_ptr(),
+            LSE.data_ptr(), plan.items.data_ptr(), plan.info, d_kv, D_H, dcode, float(scale),
+            ws.data_ptr() if ws.numel() else None, ws.numel(), st))
+        ctx.save_for_backward(q_raw, W_Q, W_K, q_proj, X, W_V, O, LSE)
+        ctx.plan = plan
+        ctx.scale = scale
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):
+        q_raw, W_Q, W_K, q_proj, X, W_V, O, LSE = ctx.saved_tensors
+        T_q, d_q = q_raw.shape
+        d_kv, H, D_H = W_K.shape
+        L = _lib.lib()
+        st = _lib.stream_ptr(X.device)
+        u = torch.empty((T_q, H, d_kv), dtype=q_raw.dtype, device=X.device)
+        _lib.check(L.vafa_absorb_project_u(q_proj.data_ptr(), W_K.data_ptr(), u.data_ptr(), T_q,
+                                           H, d_kv, D_H, _lib.dtype_code(u.dtype), st))
+        du, dX, dW_V = _absorb_bwd(u, X, W_V, O, LSE, dO, ctx.plan, ctx.scale)
+        need_q, _, need_wq, need_wk = ctx.needs_input_grad[:4]
+        dq = torch.empty_like(q_raw) if need_q else None
+        dwq = torch.empty_like(W_Q) if need_wq else None
+        dwk = torch.empty_like(W_K) if need_wk else None
+        if need_q or need_wq or need_wk:
+            ws = _workspace(L.vafa_absorb_project_workspace(T_q, H, d_q, d_kv, D_H, 1), X.device)
+            _lib.check(L.vafa_absorb_project_bwd(
+                q_raw.data_ptr(), W_Q.data_ptr(), W_K.data_ptr(), q_proj.data_ptr(),
+                du.data_ptr(), _lib.ptr(dq), _lib.ptr(dwq), _lib.ptr(dwk), T_q, H, d_q, d_kv,
+                D_H, _lib.dtype_code(du.dtype), ws.data_ptr(), ws.numel(), st))
+        return dq, dX, dwq, dwk, dW_V, None, None, None, None, None, None
+
+
 def _project_u(q_raw: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor) -> torch.Tensor:
     """u[t,h,:] = (q_raw[t] W_Q[:,h,:]) W_K[:,h,:]^T (ta/interface.py:434-435),
     contiguous ``[T_q, H, d_kv]``.
@@ -366,9 +461,13 @@ def packed_target_attn(
         q_raw, X, W_Q, W_K, W_V = (t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
                                    for t in (q_raw, X, W_Q, W_K, W_V))
 
-    u = _project_u(q_raw, W_Q, W_K)
     if scale is None:
         scale = 1.0 / math.sqrt(D_H)
+    if _fold_native(q_raw, X, W_Q, W_K, W_V):
+        return _FoldedTargetAttn.apply(
+            q_raw, X, W_Q, W_K, W_V, cu_seqlens_q, cu_seqlens_k, float(scale),
+            q_chunk_indices, k_chunk_indices, validate)
+    u = _project_u(q_raw, W_Q, W_K)
     return target_attn_inner(
         u, X, W_V, cu_seqlens_q, cu_seqlens_k, scale,
         q_chunk_indices=q_chunk_indices, k_chunk_indices=k_chunk_indices, validate=validate)

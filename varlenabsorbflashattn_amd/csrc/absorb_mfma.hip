@@ -14,6 +14,13 @@
 // loop each wave rounds aX/l to the input dtype in registers and projects it
 // by its heads' W_V (16x16x32 products, W_V^T stored in the accumulators'
 // f order): no LDS staging and no barrier in the epilogue.
+//
+// Folded projection (FOLD): instead of reading u (T_q x H x D_KV, written by
+// a projection launch), the prologue forms each lane's u row from q_proj
+// (T_q x H x D_H, 1/8 of u's bytes at D_KV = 256, D_H = 32) and W_K on the
+// matrix cores -- U^T_h = W_K,h q_proj_h^T per 16-row f tile, accumulated in
+// fp32 over d and rounded once to the input dtype, the reference's u GEMM
+// (ta/interface.py:435) -- so u never reaches HBM.
 #include "absorb_tiles.h"
 
 namespace vafa {
@@ -43,13 +50,30 @@ __global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__
   wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
 }
 
+// W_K [F, H, DH] -> wkt [H, FP, DHP] (DHP = max(DH, 32); zeros at f >= F and
+// d >= DH): one 16-byte A-operand load per (f row, 8 d) of the folded
+// projection, with the rows of one head contiguous.
+template <typename T>
+__global__ __launch_bounds__(256) void relayout_wk_kernel(const T *__restrict__ wk,
+                                                          T *__restrict__ wkt, int H, int F,
+                                                          int DH, int FP, int DHP) {
+  const int64_t n = (int64_t)H * FP * DHP;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int d = (int)(i % DHP);
+  const int f = (int)((i / DHP) % FP);
+  const int h = (int)(i / ((int64_t)DHP * FP));
+  wkt[i] = (f < F && d < DH) ? wk[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
+}
+
 constexpr int kFwdWaves = 4;  // 4 waves x 16 rows = kAbsorbRows
 
-template <typename T, int FP, int DH>
+template <typename T, int FP, int DH, bool FOLD>
 __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
-    const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ wvt,
-    T *__restrict__ O, float *__restrict__ lse, float *__restrict__ part_o,
-    float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, int F, float c) {
+    const T *__restrict__ u, const T *__restrict__ wkt, const T *__restrict__ X,
+    const T *__restrict__ wvt, T *__restrict__ O, float *__restrict__ lse,
+    float *__restrict__ part_o, float *__restrict__ part_lse, const int32_t *__restrict__ items,
+    int H, int F, float c) {
   using M16 = Mfma16<T>;
   using v8 = typename Mfma<T>::v8;
   using S = AbsSmem<FP>;
@@ -91,7 +115,59 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 
   // U^T fragments (B operand of S^T = X U^T): row `row`, f = 32*kc + 8*lq + t
   v8 uf[NK];
-  {
+  if constexpr (FOLD) {
+    // q_proj fragments (B operand of U^T = W_K,h q_proj^T): row `row`,
+    // d = 32*ks + 8*lq + t; rows past the item's tokens and d >= DH read zeros
+    constexpr int DHP = DH < 32 ? 32 : DH;
+    constexpr int NKS = DHP / 32;
+    v8 qb[NKS];
+    const rsrc_t rq = make_rsrc(u + (int64_t)t0 * H * DH, (int64_t)nrows * DH * 2);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 32 * ks + 8 * lq;
+      u32x4 w = buf_load16(rq, d0 < DH ? ((tl * H + hh) * DH + d0) * 2 : 0x7fffffff);
+      asm volatile("" : "+v"(w));
+      qb[ks] = as_v8<T>(w);
+    }
+    // Output tile (kc, s) of U^T: its row m holds f = 32*kc + 8*(m/4) + 4*s
+    // + m%4, so lane (column l16, group lq) receives f = 32*kc + 8*lq + 4*s + r
+    // (r < 4): elements 4*s + r of the B fragment uf[kc] above.  A wave's 16
+    // rows span at most two heads: with two, both heads' products are formed
+    // and each lane keeps its own head's.  A negative scale is folded into u
+    // (an exact sign flip before the rounding).
+    const int h_first = (wave * 16) / TT;
+    const bool two = TT < 16;
+    const float sgn = c < 0.f ? -1.f : 1.f;
+    const bool mine0 = hh == h_first;
+    const int frow = 8 * (l16 >> 2) + (l16 & 3);
+    const T *wa0 = wkt + ((int64_t)h_first * FP + frow) * DHP + 8 * lq;
+    const T *wa1 = wa0 + (int64_t)FP * DHP;
+#pragma unroll
+    for (int kc = 0; kc < NK; ++kc) {
+      u32x4 a0[2][NKS], a1[2][NKS];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int64_t off = (int64_t)(32 * kc + 4 * s) * DHP + 32 * ks;
+          a0[s][ks] = *reinterpret_cast<const u32x4 *>(wa0 + off);
+          if (two) a1[s][ks] = *reinterpret_cast<const u32x4 *>(wa1 + off);
+        }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) r0 = M16::mma(as_v8<T>(a0[s][ks]), qb[ks], r0);
+        if (two) {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) r1 = M16::mma(as_v8<T>(a1[s][ks]), qb[ks], r1);
+        }
+        const f32x4 r = (!two || mine0) ? r0 : r1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) uf[kc][4 * s + e] = static_cast<T>(r[e] * sgn);
+      }
+    }
+  } else {
     const rsrc_t ru = make_rsrc(u + (int64_t)t0 * H * F, (int64_t)nrows * F * 2);
     const int fchunks = F / 8;
     // a negative scale is folded into u (sign flip of every element)
@@ -269,13 +345,22 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 }
 
 
+template <typename T, int FP, int DH, bool FOLD>
+void launch_fold(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
+  const int smem = AbsSmem<FP>::kLoopBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH, FOLD>), smem);
+  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH, FOLD>), dim3((unsigned)a.n_items),
+                     dim3(64 * kFwdWaves), smem, st, (const T *)a.u, (const T *)a.wkt,
+                     (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o, a.part_lse, a.items, a.H,
+                     a.F, a.scale * kLog2e);
+}
+
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
-  const int smem = AbsSmem<FP>::kLoopBytes;
-  allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH>), smem);
-  hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH>), dim3((unsigned)a.n_items), dim3(64 * kFwdWaves),
-                     smem, st, (const T *)a.u, (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o,
-                     a.part_lse, a.items, a.H, a.F, a.scale * kLog2e);
+  if (a.fold)
+    launch_fold<T, FP, DH, true>(a, wvt, st);
+  else
+    launch_fold<T, FP, DH, false>(a, wvt, st);
 }
 
 template <typename T, int DH>
@@ -309,6 +394,9 @@ bool mfma_absorb_supported(int H, int F, int DH) {
 }
 
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH) { return (int64_t)H * DH * padded_f(F); }
+int64_t mfma_absorb_wkt_elems(int H, int F, int DH) {
+  return (int64_t)H * padded_f(F) * (DH < 32 ? 32 : DH);
+}
 
 template <typename T>
 void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
@@ -317,6 +405,13 @@ void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
   const int64_t n = (int64_t)a.H * a.DH * FP;
   hipLaunchKernelGGL(transpose_wv_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                      (const T *)a.wv, wvt, a.H, a.F, a.DH, FP);
+  if (a.fold) {
+    const int DHP = a.DH < 32 ? 32 : a.DH;
+    const int64_t nk = (int64_t)a.H * FP * DHP;
+    hipLaunchKernelGGL(relayout_wk_kernel<T>, dim3((unsigned)((nk + 255) / 256)), dim3(256), 0,
+                       st, (const T *)a.wk, reinterpret_cast<T *>(a.wkt), a.H, a.F, a.DH, FP,
+                       DHP);
+  }
   if (a.n_items == 0) return;
   switch (a.DH) {
     case 16: launch_dh<T, 16>(a, wvt, FP, st); break;

@@ -50,8 +50,10 @@ int check_info(const vafa_plan_info *info, int64_t kind) {
 }
 
 // A varlen plan's tiles must be ones the kernels of this head dim run: the
-// planner picks 256-row query tiles only for D <= 128 and 256-key tiles only
-// for D = 128 (D=16 runs on the D=32 kernels).
+// planner picks 256-row query tiles only for D <= 128, 256-key tiles only
+// for D = 128 (D=16 runs on the D=32 kernels), and fused key-major items
+// (chunks of kFusedTiles key tiles) only for D <= kFusedMaxD -- the plain
+// dK/dV kernels of a wider head dim cover one key tile per item.
 int check_varlen_tiles(const vafa_plan_info *info, int64_t D) {
   const int64_t Dk = D == 16 ? 32 : D;
   const bool q_ok =
@@ -63,6 +65,11 @@ int check_varlen_tiles(const vafa_plan_info *info, int64_t D) {
                 "plan tiles (%lld queries, %lld keys) do not fit head_dim %lld: build the "
                 "plan with this head_dim",
                 (long long)info->q_tile, (long long)info->k_tile, (long long)D);
+  if (info->n_fkv > 0 && Dk > kFusedMaxD)
+    return fail(VAFA_ERR_VALUE,
+                "plan holds fused key-major items, which head_dim %lld does not run: build "
+                "the plan with this head_dim",
+                (long long)D);
   return VAFA_OK;
 }
 
@@ -195,20 +202,14 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
     }
     if (!mfma) launch_simt_varlen_dkv<T>(a, st);
     if (!fq && a.n_fkv > 0) {
-      // fused-planned key tiles on the plain dK/dV kernels ({k0, k1, q0, q1}
-      // leads both item formats)
+      // fused-planned chunks without the fused kernel (fp32): the wave-per-key
+      // dK/dV kernel walks any key range ({k0, k1, q0, q1} leads both item
+      // formats).  16-bit operands always take the fused kernel here: a plan
+      // holds fused items only for D <= kFusedMaxD (check_varlen_tiles).
       VarlenArgs kv = a;
       kv.kv_items = a.fkv_items;
       kv.n_kv = a.n_fkv;
-      if constexpr (sizeof(T) == 2) {
-        if (mfma) {
-          if (a.D == 32) launch_mfma_varlen_dkv<T, 32>(kv, st);
-          if (a.D == 64) launch_mfma_varlen_dkv<T, 64>(kv, st);
-          if (a.D == 128) launch_mfma_varlen_dkv<T, 128>(kv, st);
-          if (a.D == 256) launch_mfma_varlen_dkv<T, 256>(kv, st);
-        }
-      }
-      if (!mfma) launch_simt_varlen_dkv<T>(kv, st);
+      launch_simt_varlen_dkv<T>(kv, st);
     }
   }
 }
@@ -230,14 +231,15 @@ void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
 struct AbsorbWs {
   float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *dax = nullptr, *ax = nullptr,
         *dwv_part = nullptr;
-  void *wvt = nullptr;
+  void *wvt = nullptr, *wkt = nullptr;
   int64_t n_tchunks = 0, tchunk = 0;
   int64_t bytes = 0;
 };
 
 constexpr int64_t kDwvChunks = 64;
 
-AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t DH, bool bwd) {
+AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t DH, bool bwd,
+                      bool fold = false) {
   Carver c(ws);
   AbsorbWs w;
   const int64_t H = info->H, Tq = info->T_q;
@@ -249,6 +251,8 @@ AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t D
     const int64_t wvt16 = mfma_absorb_wvt_elems((int)H, (int)F, (int)DH) * 2;
     const int64_t wvt32 = f32_absorb_wvt_elems((int)H, (int)F, (int)DH) * 4;
     w.wvt = c.take<char>(wvt16 > wvt32 ? wvt16 : wvt32);
+    // folded projection: W_K re-laid out per head (16-bit only)
+    if (fold) w.wkt = c.take<char>(mfma_absorb_wkt_elems((int)H, (int)F, (int)DH) * 2);
   } else {
     w.delta = c.take<float>(Tq * H * 4);
     w.dax = c.take<float>(Tq * H * F * 4);
@@ -437,7 +441,7 @@ void project_fwd(const void *q_raw, const void *W_Q, const void *W_K, void *q_pr
   // q_proj [T, HD] = q_raw [T, DQ] . W_Q [DQ, HD], through W_Q^T [HD, DQ]
   launch_transpose2d<T>(W_Q, w.wt, DQ, HD, st);
   launch_rowgemm<T>(RowGemm{q_raw, w.wt, q_proj, T_q, 1, HD, DQ, DQ, 0, 0, DQ, HD, 0}, st);
-  project_u<T>(q_proj, W_K, u, T_q, H, F, DH, st);
+  if (u != nullptr) project_u<T>(q_proj, W_K, u, T_q, H, F, DH, st);
 }
 
 template <typename T>
@@ -674,6 +678,53 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
   if (int rc = by_dtype<AFwd>(dtype, a, (hipStream_t)stream)) return rc;
   return check_launch("vafa_absorb_fwd");
+}
+
+// The folded forward runs on the 16-bit matrix-core kernel only (the
+// projection it folds is the 16-bit one of vafa_absorb_project_fwd).
+static bool fold_supported(int64_t H, int64_t F, int64_t DH, int32_t dtype) {
+  if (dtype != VAFA_BF16 && dtype != VAFA_F16) return false;
+  if (H < 1 || H > 64 || F < 1 || F > 512 || DH < 1 || DH > 256) return false;
+  return mfma_absorb_supported<bf16>((int)H, (int)F, (int)DH);
+}
+
+int vafa_absorb_fold_supported(int64_t H, int64_t D_KV, int64_t D_H, int32_t dtype) {
+  return fold_supported(H, D_KV, D_H, dtype) ? 1 : 0;
+}
+
+int64_t vafa_absorb_fwd_fold_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H) {
+  if (check_info(info, 2)) return -1;
+  return carve_absorb(nullptr, info, D_KV, D_H, false, true).bytes;
+}
+
+int vafa_absorb_fwd_fold(const void *q_proj, const void *W_K, const void *X, const void *W_V,
+                         void *O, float *lse, const int32_t *plan_dev,
+                         const vafa_plan_info *info, int64_t D_KV, int64_t D_H, int32_t dtype,
+                         float scale, void *workspace, int64_t workspace_bytes, void *stream) {
+  if (int rc = check_info(info, 2)) return rc;
+  if (int rc = check_absorb_dims(D_KV, D_H)) return rc;
+  if (!fold_supported(info->H, D_KV, D_H, dtype))
+    return fail(VAFA_ERR_VALUE,
+                "absorb_fwd_fold: H=%lld, D_KV=%lld, D_H=%lld, dtype %d is not a shape of the "
+                "folded kernel (vafa_absorb_fold_supported); use vafa_absorb_project_fwd + "
+                "vafa_absorb_fwd",
+                (long long)info->H, (long long)D_KV, (long long)D_H, (int)dtype);
+  if (int rc = check_aligned("absorb_fwd_fold", {q_proj, W_K, X, W_V, O})) return rc;
+  AbsorbWs w = carve_absorb(workspace, info, D_KV, D_H, false, true);
+  if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
+    return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)w.bytes);
+  AbsorbArgs a{};
+  a.u = q_proj; a.wk = W_K; a.wkt = w.wkt; a.fold = true;
+  a.X = X; a.wv = W_V; a.O = O; a.lse = lse;
+  a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt;
+  a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
+  a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
+  a.comb_rows = (int)info->max_comb_rows;
+  a.T_q = info->T_q; a.T_k = info->T_k;
+  a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
+  if (int rc = by_dtype<AFwd>(dtype, a, (hipStream_t)stream)) return rc;
+  return check_launch("vafa_absorb_fwd_fold");
 }
 
 int vafa_absorb_project_u(const void *q_proj, const void *W_K, void *u, int64_t T_q, int64_t H,

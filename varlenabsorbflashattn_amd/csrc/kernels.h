@@ -54,6 +54,13 @@ struct AbsorbArgs {
   float *ax;                  // aX [T_q, H, F] fp32 (backward, for dW_V)
   float *dwv_part;            // [n_tchunks, F, H, D_H] fp32 (backward)
   void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
+  // Folded projection (forward): `u` holds q_proj [T_q, H, D_H] instead of u,
+  // and each workgroup forms its rows' u = q_proj_h W_K,h^T from `wk`
+  // (W_K [F, H, D_H]) re-laid out into `wkt` ([H, F padded to 32, D_H padded
+  // to 32], zeros in the padding).
+  const void *wk;
+  void *wkt;
+  bool fold;
   const int32_t *items, *comb_items, *kv_items, *qseg_items;
   int64_t n_items, n_comb, n_kv, n_qseg;
   int64_t n_kv_res;           // leading kv items for absorb_dx_res_kernel
@@ -117,6 +124,7 @@ template <typename T, int D> void launch_mfma_varlen_fkv(const VarlenArgs &, hip
 // absorb_mfma.hip (bf16 / f16)
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
+int64_t mfma_absorb_wkt_elems(int H, int F, int DH);
 template <typename T> void launch_mfma_absorb_fwd(const AbsorbArgs &, hipStream_t);
 
 // absorb_project.hip (bf16 / f16): Y[t, g*ys + j] = sum_k X[t*ldx + g*xs + k]

@@ -243,10 +243,13 @@ def bench_absorb(case, iters, d_q=None, full=False, dtype=None):
     """Inner absorb forward on precomputed u, through the reference's hot-path
     contract: prepare_target_attn_indices once, then validate=False calls
     (ta/interface.py:125-138) -- no host round trip inside the timed loop.
-    With ``full``, also times the whole packed_target_attn forward (u
-    projection included) on the same inputs; returns (inner, full) stats."""
+    With ``full``, also times the whole packed_target_attn forward on the
+    same inputs (16-bit: q_proj, then the attention with u formed inside the
+    kernel) and the unfused whole op (projection kernels write u, then the
+    inner op reads it); returns (inner, full, unfused) stats."""
     import torch
     from varlenabsorbflashattn_amd import packed_target_attn, target_attn_inner
+    from varlenabsorbflashattn_amd.absorb import _project_u
     q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case, d_q, dtype)
     scale = 1.0 / math.sqrt(case.D_H)
 
@@ -263,10 +266,16 @@ def bench_absorb(case, iters, d_q=None, full=False, dtype=None):
                                    q_chunk_indices=qi, k_chunk_indices=ki, scale=scale,
                                    validate=False)
 
+        def unfused_fwd():
+            with torch.no_grad():
+                uu = _project_u(q_raw, W_Q, W_K)
+                target_attn_inner(uu, X, W_V, cq, ck, scale, qi, ki, validate=False)
+
         full_st = timed(full_fwd, iters)
+        unf_st = timed(unfused_fwd, iters)
     del q_raw, X, u
     torch.cuda.empty_cache()
-    return (st, full_st) if full else st
+    return (st, full_st, unf_st) if full else st
 
 
 def bench_absorb_bwd(case, iters, d_q=None, dtype=None):
@@ -298,17 +307,23 @@ def bench_absorb_bwd(case, iters, d_q=None, dtype=None):
     return st, f_st
 
 
-def bench_absorb_full(case, iters):
+def bench_absorb_full(case, iters, unfused=False):
     """The whole packed_target_attn (projections included) through the
-    prepared-index contract: returns (fwd+bwd, fwd) stats."""
+    prepared-index contract: returns (fwd+bwd, fwd) stats.  With
+    ``unfused``, the op is composed of the projection (u written) and the
+    inner op instead of taking the folded forward."""
     import torch
-    from varlenabsorbflashattn_amd import packed_target_attn
+    from varlenabsorbflashattn_amd import packed_target_attn, target_attn_inner
+    from varlenabsorbflashattn_amd.absorb import _project_u
     q_raw, X, W_Q, W_K, W_V, u, cq, ck, qi, ki = _absorb_setup(case)
     ins = [t.detach().clone().requires_grad_(True) for t in (q_raw, X, W_Q, W_K, W_V)]
     g = torch.Generator().manual_seed(1)
     dO = torch.randn(u.shape[0], case.H, case.D_H, generator=g).to(u.device, u.dtype)
 
     def call():
+        if unfused:
+            uu = _project_u(ins[0], ins[2], ins[3])
+            return target_attn_inner(uu, ins[1], ins[4], cq, ck, None, qi, ki, validate=False)
         return packed_target_attn(*ins, cu_seqlens_q=cq, cu_seqlens_k=ck, q_chunk_indices=qi,
                                   k_chunk_indices=ki, validate=False)
 
@@ -328,13 +343,16 @@ def bench_absorb_full(case, iters):
     return st, f_st
 
 
-def absorb_line(case, st, full_st=None):
+def absorb_line(case, st, full_st=None, unf_st=None):
     gbs = case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9
     out = {"ms": st, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+           "GB/s_p50": case.bytes_fwd() / (st["p50"] * 1e-3) / 1e9,
            "TFLOP/s": case.flops_fwd / (st["mean"] * 1e-3) / 1e12,
            "sum_lq": int(sum(case.q_lens)), "sum_lk": int(sum(case.k_lens))}
     if full_st is not None:
         out["packed_target_attn_ms"] = full_st
+    if unf_st is not None:
+        out["packed_target_attn_unfused_ms"] = unf_st
     return out
 
 
@@ -485,7 +503,9 @@ def run_only(which, steps, warmup):
     if which == "c4full":
         case = W.config4(seed=0)
         st, f_st = bench_absorb_full(case, max(steps, 1))
-        return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st}
+        u_st, uf_st = bench_absorb_full(case, max(steps, 1), unfused=True)
+        return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st,
+                "unfused_fwd_bwd_ms": u_st, "unfused_fwd_ms": uf_st}
     if which in ("c4b", "c4_fp32"):
         case = W.config4(seed=0)
         dt = torch.float32 if which == "c4_fp32" else None
@@ -493,8 +513,8 @@ def run_only(which, steps, warmup):
         return {"config": case.name + ("_fp32" if dt else "") + "_fwd_bwd", "ms": st,
                 "fwd_ms": f_st, "bwd_ms": st["mean"] - f_st["mean"]}
     case = W.config4(seed=0) if which == "c4" else W.config5(seed=0)
-    st = bench_absorb(case, max(steps, 1))
-    return {"config": case.name, **absorb_line(case, st)}
+    st, full_st, unf_st = bench_absorb(case, max(steps, 1), full=True)
+    return {"config": case.name, **absorb_line(case, st, full_st, unf_st)}
 
 
 def main():
@@ -542,8 +562,8 @@ def main():
             "TFLOP/s": c3.flops_fwd / (c3_st["mean"] * 1e-3) / 1e12}
         log("C3", c3_st["mean"], gbs)
         for cfg in (W.config4(seed=0), W.config5(seed=0)):
-            st, full_st = bench_absorb(cfg, n2, full=True)
-            secondary[cfg.name + "_fwd"] = absorb_line(cfg, st, full_st)
+            st, full_st, unf_st = bench_absorb(cfg, n2, full=True)
+            secondary[cfg.name + "_fwd"] = absorb_line(cfg, st, full_st, unf_st)
             log(cfg.name, st["mean"], secondary[cfg.name + "_fwd"]["GB/s"])
         c4 = W.config4(seed=0)
         b_st, bf_st = bench_absorb_bwd(c4, n2)

@@ -35,40 +35,41 @@ using namespace absorb;
 // position 8a + b holds f = 4a + b (b < 4) or 16 + 4a + b - 4 (b >= 4), the
 // order in which the forward's accumulators present aX^T (rows 4a..4a+3 of
 // the chunk's two 16-row tiles).
-template <typename T>
-__global__ __launch_bounds__(256) void transpose_wv_kernel(const T *__restrict__ wv,
-                                                           T *__restrict__ wvt, int H, int F,
-                                                           int DH, int FP) {
-  const int64_t n = (int64_t)H * DH * FP;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int p = (int)(i % FP);
-  const int d = (int)((i / FP) % DH);
-  const int h = (int)(i / ((int64_t)FP * DH));
-  const int a = (p & 31) >> 3, b = p & 7;
-  const int f = (p & ~31) + (b < 4 ? 4 * a + b : 16 + 4 * a + b - 4);
-  wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
-}
-
+// With the folded projection the same launch also writes
 // W_K [F, H, DH] -> wkt [H, FP, DHP] (DHP = max(DH, 32); zeros at f >= F and
-// d >= DH): one 16-byte A-operand load per (f row, 8 d) of the folded
-// projection, with the rows of one head contiguous.
+// d >= DH): the rows of one head contiguous, so the u product's A operand
+// (16 f rows x 16 bytes per lane group) reads whole cache lines.
 template <typename T>
-__global__ __launch_bounds__(256) void relayout_wk_kernel(const T *__restrict__ wk,
+__global__ __launch_bounds__(256) void transpose_w_kernel(const T *__restrict__ wv,
+                                                          T *__restrict__ wvt,
+                                                          const T *__restrict__ wk,
                                                           T *__restrict__ wkt, int H, int F,
                                                           int DH, int FP, int DHP) {
-  const int64_t n = (int64_t)H * FP * DHP;
+  const int64_t nv = (int64_t)H * DH * FP;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int d = (int)(i % DHP);
-  const int f = (int)((i / DHP) % FP);
-  const int h = (int)(i / ((int64_t)DHP * FP));
-  wkt[i] = (f < F && d < DH) ? wk[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
+  if (i < nv) {
+    const int p = (int)(i % FP);
+    const int d = (int)((i / FP) % DH);
+    const int h = (int)(i / ((int64_t)FP * DH));
+    const int a = (p & 31) >> 3, b = p & 7;
+    const int f = (p & ~31) + (b < 4 ? 4 * a + b : 16 + 4 * a + b - 4);
+    wvt[i] = f < F ? wv[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
+    return;
+  }
+  if (wkt == nullptr) return;
+  const int64_t j = i - nv;
+  if (j >= (int64_t)H * FP * DHP) return;
+  const int d = (int)(j % DHP);
+  const int f = (int)((j / DHP) % FP);
+  const int h = (int)(j / ((int64_t)DHP * FP));
+  wkt[j] = (f < F && d < DH) ? wk[((int64_t)f * H + h) * DH + d] : static_cast<T>(0.f);
 }
 
 constexpr int kFwdWaves = 4;  // 4 waves x 16 rows = kAbsorbRows
 
-template <typename T, int FP, int DH, bool FOLD>
+// FOLD: 0 = read u; 1 = form u in the prologue, one head per wave (H <= 4);
+// 2 = form u, two heads per wave (H = 8: 8 tokens per head, 16 rows a wave).
+template <typename T, int FP, int DH, int FOLD>
 __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
     const T *__restrict__ u, const T *__restrict__ wkt, const T *__restrict__ X,
     const T *__restrict__ wvt, T *__restrict__ O, float *__restrict__ lse,
@@ -115,56 +116,77 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 
   // U^T fragments (B operand of S^T = X U^T): row `row`, f = 32*kc + 8*lq + t
   v8 uf[NK];
-  if constexpr (FOLD) {
+  if constexpr (FOLD != 0) {
     // q_proj fragments (B operand of U^T = W_K,h q_proj^T): row `row`,
     // d = 32*ks + 8*lq + t; rows past the item's tokens and d >= DH read zeros
     constexpr int DHP = DH < 32 ? 32 : DH;
     constexpr int NKS = DHP / 32;
     v8 qb[NKS];
     const rsrc_t rq = make_rsrc(u + (int64_t)t0 * H * DH, (int64_t)nrows * DH * 2);
+    // (consumed in the prologue, so no wait is forced here: the first W_K
+    // batch below is requested before the first product waits for q_proj)
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d0 = 32 * ks + 8 * lq;
-      u32x4 w = buf_load16(rq, d0 < DH ? ((tl * H + hh) * DH + d0) * 2 : 0x7fffffff);
-      asm volatile("" : "+v"(w));
-      qb[ks] = as_v8<T>(w);
+      qb[ks] = as_v8<T>(buf_load16(rq, d0 < DH ? ((tl * H + hh) * DH + d0) * 2 : 0x7fffffff));
     }
     // Output tile (kc, s) of U^T: its row m holds f = 32*kc + 8*(m/4) + 4*s
     // + m%4, so lane (column l16, group lq) receives f = 32*kc + 8*lq + 4*s + r
-    // (r < 4): elements 4*s + r of the B fragment uf[kc] above.  A wave's 16
-    // rows span at most two heads: with two, both heads' products are formed
-    // and each lane keeps its own head's.  A negative scale is folded into u
-    // (an exact sign flip before the rounding).
+    // (r < 4): elements 4*s + r of the B fragment uf[kc] above.  With two
+    // heads in a wave (FOLD = 2) both heads' products are formed and each
+    // lane keeps its own head's.  A negative scale is folded into u (an exact
+    // sign flip before the rounding).  The A operands (16-byte rows of wkt,
+    // from L2) are loaded KB chunks at a time, the next batch in flight
+    // while the current one is multiplied: one L2 round trip of latency
+    // instead of one per chunk.
+    constexpr int NHW = FOLD == 2 ? 2 : 1;      // heads per wave
+    constexpr int KB = 2;                       // 32-wide f chunks per batch
+    constexpr int NB = (NK + KB - 1) / KB;      // the last batch may be short
     const int h_first = (wave * 16) / TT;
-    const bool two = TT < 16;
     const float sgn = c < 0.f ? -1.f : 1.f;
     const bool mine0 = hh == h_first;
     const int frow = 8 * (l16 >> 2) + (l16 & 3);
-    const T *wa0 = wkt + ((int64_t)h_first * FP + frow) * DHP + 8 * lq;
-    const T *wa1 = wa0 + (int64_t)FP * DHP;
+    const T *wa = wkt + ((int64_t)h_first * FP + frow) * DHP + 8 * lq;
+    u32x4 abuf[2][KB][2][NHW][NKS];
+    auto load_batch = [&](int b, int slot) {
 #pragma unroll
-    for (int kc = 0; kc < NK; ++kc) {
-      u32x4 a0[2][NKS], a1[2][NKS];
+      for (int kk = 0; kk < KB; ++kk)
+        if (b * KB + kk < NK)
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const int64_t off = (int64_t)(32 * kc + 4 * s) * DHP + 32 * ks;
-          a0[s][ks] = *reinterpret_cast<const u32x4 *>(wa0 + off);
-          if (two) a1[s][ks] = *reinterpret_cast<const u32x4 *>(wa1 + off);
+          for (int hx = 0; hx < NHW; ++hx)
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+              abuf[slot][kk][s][hx][ks] = *reinterpret_cast<const u32x4 *>(
+                  wa + ((int64_t)hx * FP + 32 * (b * KB + kk) + 4 * s) * DHP + 32 * ks);
+    };
+    load_batch(0, 0);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b + 1 < NB) load_batch(b + 1, (b + 1) & 1);
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) {
+        const int kc = b * KB + kk;
+        if (kc >= NK) break;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          f32x4 r[NHW];
+#pragma unroll
+          for (int hx = 0; hx < NHW; ++hx) {
+            r[hx] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+              r[hx] = M16::mma(as_v8<T>(abuf[b & 1][kk][s][hx][ks]), qb[ks], r[hx]);
+          }
+          f32x4 rr = r[0];
+          if constexpr (NHW == 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rr[e] = mine0 ? r[0][e] : r[1][e];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) uf[kc][4 * s + e] = static_cast<T>(rr[e] * sgn);
         }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) r0 = M16::mma(as_v8<T>(a0[s][ks]), qb[ks], r0);
-        if (two) {
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) r1 = M16::mma(as_v8<T>(a1[s][ks]), qb[ks], r1);
-        }
-        const f32x4 r = (!two || mine0) ? r0 : r1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) uf[kc][4 * s + e] = static_cast<T>(r[e] * sgn);
       }
     }
   } else {
@@ -345,7 +367,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 }
 
 
-template <typename T, int FP, int DH, bool FOLD>
+template <typename T, int FP, int DH, int FOLD>
 void launch_fold(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   const int smem = AbsSmem<FP>::kLoopBytes;
   allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH, FOLD>), smem);
@@ -357,10 +379,12 @@ void launch_fold(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
 
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
-  if (a.fold)
-    launch_fold<T, FP, DH, true>(a, wvt, st);
+  if (!a.fold)
+    launch_fold<T, FP, DH, 0>(a, wvt, st);
+  else if (kAbsorbRows / a.H < 16)  // 8 tokens per head: two heads per wave
+    launch_fold<T, FP, DH, 2>(a, wvt, st);
   else
-    launch_fold<T, FP, DH, false>(a, wvt, st);
+    launch_fold<T, FP, DH, 1>(a, wvt, st);
 }
 
 template <typename T, int DH>
@@ -402,16 +426,11 @@ template <typename T>
 void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
   const int FP = padded_f(a.F);
   T *wvt = reinterpret_cast<T *>(a.wvt);
-  const int64_t n = (int64_t)a.H * a.DH * FP;
-  hipLaunchKernelGGL(transpose_wv_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                     (const T *)a.wv, wvt, a.H, a.F, a.DH, FP);
-  if (a.fold) {
-    const int DHP = a.DH < 32 ? 32 : a.DH;
-    const int64_t nk = (int64_t)a.H * FP * DHP;
-    hipLaunchKernelGGL(relayout_wk_kernel<T>, dim3((unsigned)((nk + 255) / 256)), dim3(256), 0,
-                       st, (const T *)a.wk, reinterpret_cast<T *>(a.wkt), a.H, a.F, a.DH, FP,
-                       DHP);
-  }
+  const int DHP = a.DH < 32 ? 32 : a.DH;
+  const int64_t n = (int64_t)a.H * a.DH * FP + (a.fold ? (int64_t)a.H * FP * DHP : 0);
+  hipLaunchKernelGGL(transpose_w_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     (const T *)a.wv, wvt, (const T *)a.wk,
+                     a.fold ? reinterpret_cast<T *>(a.wkt) : nullptr, a.H, a.F, a.DH, FP, DHP);
   if (a.n_items == 0) return;
   switch (a.DH) {
     case 16: launch_dh<T, 16>(a, wvt, FP, st); break;

@@ -194,14 +194,16 @@ def replay_records():
     return stage1, ta
 
 
-def bench_replay(steps, warmup):
+def bench_replay(steps, warmup, n_stage1=None, n_ta=None):
     """Varlen fwd / fwd+bwd on the stage-1 serving shapes at H=4, D=64
     (fa-tools/benchmark_packed_varlen_flash_attn.py:900-954) and the absorb
     inner op on the real target-attention shapes, d_q=968, d_kv=216
-    (ta/test_smoke.py:467-534), bf16."""
+    (ta/test_smoke.py:467-534), bf16; the first n_stage1 / n_ta records of
+    each (all by default)."""
     import torch
     from varlenabsorbflashattn_amd import workloads as W
     stage1, ta = replay_records()
+    stage1, ta = stage1[:n_stage1], ta[:n_ta]
     out = {"config": "replay", "stage1_H4_D64": [], "ta_real_dq968_dkv216": []}
     for r in stage1:
         case = W.VarlenCase(r["name"], r["q_lens"], r["k_lens"], 4, 64, torch.bfloat16)
@@ -380,6 +382,30 @@ def _cpu_model():
     return None
 
 
+def _cpu_topology():
+    """lscpu's model, sockets, cores per socket, threads per core and CPU
+    count, plus the CPUs this process may run on."""
+    import subprocess
+    out = {}
+    try:
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        keys = {"Model name": "model", "Socket(s)": "sockets",
+                "Core(s) per socket": "cores_per_socket", "Thread(s) per core": "threads_per_core",
+                "CPU(s)": "cpus", "NUMA node(s)": "numa_nodes"}
+        for line in text.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys and keys[k.strip()] not in out:
+                v = v.strip()
+                out[keys[k.strip()]] = int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        out["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    return out
+
+
 def _blas_threads():
     try:
         import threadpoolctl
@@ -451,6 +477,7 @@ def cpu_baseline():
                       f"(sum L^2 = {int(np.dot(case.q_lens, case.q_lens))}), median of "
                       f"3 runs after 1 warmup: {v_med:.2f} s",
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "lscpu": _cpu_topology(),
             "runs_s": v_runs,
             "absorb": {"sample": "first 512 of C4's 2048 samples, fp32 forward",
                        "absorbed_fwd_s": a_med, "absorbed_fwd_GB/s": gpu_bytes / a_med / 1e9,
@@ -562,12 +589,14 @@ def main():
             "TFLOP/s": c3.flops_fwd / (c3_st["mean"] * 1e-3) / 1e12}
         log("C3", c3_st["mean"], gbs)
         for cfg in (W.config4(seed=0), W.config5(seed=0)):
-            st, full_st, unf_st = bench_absorb(cfg, n2, full=True)
+            # the C4 lines last ~0.1 ms: more iterations for a stable mean
+            n_abs = 5 * n2 if cfg.name.startswith("c4") else n2
+            st, full_st, unf_st = bench_absorb(cfg, n_abs, full=True)
             secondary[cfg.name + "_fwd"] = absorb_line(cfg, st, full_st, unf_st)
             log(cfg.name, st["mean"], secondary[cfg.name + "_fwd"]["GB/s"])
         c4 = W.config4(seed=0)
-        b_st, bf_st = bench_absorb_bwd(c4, n2)
-        p_st, _ = bench_absorb_full(c4, n2)
+        b_st, bf_st = bench_absorb_bwd(c4, 3 * n2)
+        p_st, _ = bench_absorb_full(c4, 3 * n2)
         secondary[c4.name + "_fwd_bwd"] = {"ms": b_st, "fwd_ms": bf_st,
                                            "bwd_ms": b_st["mean"] - bf_st["mean"],
                                            "packed_target_attn_fwd_bwd_ms": p_st}
@@ -599,6 +628,11 @@ def main():
         s_st, f_st = bench_varlen_case(c256, n2, 3)
         secondary["varlen_d256_fwd_bwd"] = varlen_line(c256, s_st, f_st)
         log("D=256", s_st["mean"], f_st["mean"])
+        # production replay (the reference's own length fixtures): one stage-1
+        # serving record and one real absorb record
+        rep = bench_replay(n2, 3, n_stage1=1, n_ta=1)
+        secondary["replay_stage1_H4_D64"] = rep["stage1_H4_D64"][0]
+        secondary["replay_ta_real_dq968_dkv216"] = rep["ta_real_dq968_dkv216"][0]
         # D=16 (16-bit: the D=32 kernels over zero-padded copies) at C2's shape
         c16 = W.VarlenCase("c2_lengths_H16_D16", case.q_lens, case.k_lens, 16, 16,
                            torch.bfloat16)

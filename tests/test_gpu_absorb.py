@@ -86,10 +86,17 @@ def test_absorb_bf16_parity(device, name, q_lens, k_lens):
 
 
 # head counts and head dims off the benchmark shape (rows of a workgroup are
-# laid out head-major, 64 / H tokens per head)
+# laid out head-major, floor(64 / H) tokens per head)
 HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 216),
-               (2, 16, 50),   # d_kv not a multiple of 8: the wave-per-row path
-               (6, 32, 96)]   # H not dividing 64: the wave-per-row path
+               (2, 16, 50),    # d_kv not a multiple of 8: the wave-per-row path
+               (6, 32, 96),    # H not dividing 64 (10 tokens x 6 heads, 3 heads a wave)
+               (16, 32, 128),  # 4 tokens x 16 heads: 4 heads a wave
+               (12, 16, 64),   # 5 tokens x 12 heads
+               (3, 64, 256),   # 21 tokens x 3 heads
+               (5, 256, 192),  # D_H = 256 with H not dividing 64
+               (8, 256, 256),  # D_H = 256 at the benchmark width (no fold)
+               (10, 32, 256),  # 6 tokens x 10 heads, wide rows (no fold)
+               (20, 16, 64)]   # H > 16: the wave-per-row path
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32],
@@ -97,8 +104,9 @@ HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 2
 @pytest.mark.parametrize("H,D_H,d_kv", HEAD_SHAPES, ids=[f"H{h}_DH{d}_F{f}" for h, d, f in HEAD_SHAPES])
 def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
     """Matrix-core paths (bf16, fp16 and fp32) at head counts, head dims and
-    feature widths off the benchmark shape; d_kv = 50 takes the wave-per-row
-    path."""
+    feature widths off the benchmark shape, with the folded projection where
+    its kernel takes the shape; d_kv = 50 and H = 20 take the wave-per-row
+    path (16-bit), as do H not dividing 64 and D_KV > 256 for fp32."""
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)
@@ -400,10 +408,11 @@ def test_project_rejects_bad_shapes(device):
 # Folded projection (vafa_absorb_fwd_fold): packed_target_attn on 16-bit
 # matrix-core shapes forms u inside the attention kernel.  Shapes: the
 # benchmark one, one head per wave (H <= 4), D_H = 16 (half the k slots of
-# the u product are zero), D_H = 64 / 128 (two / four 32-wide k steps), and
-# feature widths that pad (216 -> 224, 192).
-FOLD_SHAPES = [(8, 32, 256), (1, 32, 64), (4, 16, 256), (2, 64, 128), (4, 128, 192),
-               (8, 64, 216)]
+# the u product are zero), D_H = 64 / 128 (two / four 32-wide k steps),
+# feature widths that pad (216 -> 224, 96 -> 128), and head counts whose
+# waves span three or four heads (H = 6: 10 tokens per head; H = 16, 12).
+FOLD_SHAPES = [(8, 32, 256), (1, 32, 64), (4, 16, 256), (2, 64, 128), (4, 128, 128),
+               (8, 64, 216), (6, 32, 96), (16, 32, 128), (12, 16, 64)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])

@@ -679,6 +679,7 @@ bool launch_mfma_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
     case 32: hipLaunchKernelGGL((absorb_dax_kernel<T, 32>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
     case 64: hipLaunchKernelGGL((absorb_dax_kernel<T, 64>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
     case 128: hipLaunchKernelGGL((absorb_dax_kernel<T, 128>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
+    case 256: hipLaunchKernelGGL((absorb_dax_kernel<T, 256>), dim3(grid), dim3(64), 0, st, (const T *)a.dO, (const T *)a.wv, (T *)a.dax, a.T_q, a.H, a.F, (const T *)a.O_in, a.delta); return true;
     default: return false;
   }
 }

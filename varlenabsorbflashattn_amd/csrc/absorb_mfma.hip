@@ -21,6 +21,8 @@
 // matrix cores -- U^T_h = W_K,h q_proj_h^T per 16-row f tile, accumulated in
 // fp32 over d and rounded once to the input dtype, the reference's u GEMM
 // (ta/interface.py:435) -- so u never reaches HBM.
+#include <algorithm>
+
 #include "absorb_tiles.h"
 
 namespace vafa {
@@ -94,13 +96,19 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   // Rows are head-major inside the workgroup: row r is token r % TT of head
   // r / TT (TT = 64 / H tokens), so a wave's 16 rows span at most two heads
   // and the W_V projection runs on the accumulators in registers.
+  // TT = floor(64 / H) tokens per item: with H not dividing 64 the last
+  // 64 - TT*H rows of the workgroup (head index >= H) stay idle.
   const int ntok = t1 - t0;
   const int nrows = ntok * H;
   const int TT = kAbsorbRows / H;
   const int row = wave * 16 + l16;
   const int tl = row % TT, hh = row / TT;  // token / head of this lane's row
-  const bool row_ok = tl < ntok;
-  const bool wave_active = (wave * 16) % TT < ntok;
+  const bool row_ok = tl < ntok && hh < H;
+  const bool wave_active = wave_any(row_ok);
+  // heads among the wave's rows
+  const int h_first = (wave * 16) / TT;
+  const int h_last = min(H - 1, (wave * 16 + 15) / TT);
+  const int nh = h_last - h_first + 1;
   const int nt = (k1 - k0 + kBK - 1) / kBK;
 
   auto issue = [&](int kb, int buf) {
@@ -128,25 +136,30 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d0 = 32 * ks + 8 * lq;
-      qb[ks] = as_v8<T>(buf_load16(rq, d0 < DH ? ((tl * H + hh) * DH + d0) * 2 : 0x7fffffff));
+      qb[ks] = as_v8<T>(
+          buf_load16(rq, d0 < DH && hh < H ? ((tl * H + hh) * DH + d0) * 2 : 0x7fffffff));
     }
     // Output tile (kc, s) of U^T: its row m holds f = 32*kc + 8*(m/4) + 4*s
     // + m%4, so lane (column l16, group lq) receives f = 32*kc + 8*lq + 4*s + r
-    // (r < 4): elements 4*s + r of the B fragment uf[kc] above.  With two
-    // heads in a wave (FOLD = 2) both heads' products are formed and each
-    // lane keeps its own head's.  A negative scale is folded into u (an exact
-    // sign flip before the rounding).  The A operands (16-byte rows of wkt,
-    // from L2) are loaded KB chunks at a time, the next batch in flight
-    // while the current one is multiplied: one L2 round trip of latency
-    // instead of one per chunk.
-    constexpr int NHW = FOLD == 2 ? 2 : 1;      // heads per wave
-    constexpr int KB = 2;                       // 32-wide f chunks per batch
-    constexpr int NB = (NK + KB - 1) / KB;      // the last batch may be short
-    const int h_first = (wave * 16) / TT;
+    // (r < 4): elements 4*s + r of the B fragment uf[kc] above.  A wave's 16
+    // rows span nh <= NHW = FOLD heads: every head's product is formed (the
+    // A operand is per head) and each lane keeps its own head's.  A negative
+    // scale is folded into u (an exact sign flip before the rounding).  The A
+    // operands (16-byte rows of wkt, from L2) are loaded KB chunks at a
+    // time, the next batch in flight while the current one is multiplied:
+    // one L2 round trip of latency instead of one per chunk.
+    constexpr int NHW = FOLD;                          // heads per wave (max)
+    constexpr int UPC = 2 * NHW * NKS;                 // A loads per f chunk
+    static_assert(UPC <= 8, "folded u product: at most 8 A loads per f chunk");
+    constexpr int KB = UPC <= 4 ? 2 : 1;               // f chunks per batch
+    constexpr int NB = (NK + KB - 1) / KB;             // the last may be short
     const float sgn = c < 0.f ? -1.f : 1.f;
-    const bool mine0 = hh == h_first;
+    const int hsel = min(max(hh - h_first, 0), NHW - 1);  // this lane's head slot
     const int frow = 8 * (l16 >> 2) + (l16 & 3);
-    const T *wa = wkt + ((int64_t)h_first * FP + frow) * DHP + 8 * lq;
+    const T *wa[NHW];
+#pragma unroll
+    for (int hx = 0; hx < NHW; ++hx)  // heads past H (idle rows) reuse the last
+      wa[hx] = wkt + ((int64_t)min(h_first + hx, H - 1) * FP + frow) * DHP + 8 * lq;
     u32x4 abuf[2][KB][2][NHW][NKS];
     auto load_batch = [&](int b, int slot) {
 #pragma unroll
@@ -159,7 +172,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks)
               abuf[slot][kk][s][hx][ks] = *reinterpret_cast<const u32x4 *>(
-                  wa + ((int64_t)hx * FP + 32 * (b * KB + kk) + 4 * s) * DHP + 32 * ks);
+                  wa[hx] + (int64_t)(32 * (b * KB + kk) + 4 * s) * DHP + 32 * ks);
     };
     load_batch(0, 0);
 #pragma unroll
@@ -180,10 +193,10 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
               r[hx] = M16::mma(as_v8<T>(abuf[b & 1][kk][s][hx][ks]), qb[ks], r[hx]);
           }
           f32x4 rr = r[0];
-          if constexpr (NHW == 2) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) rr[e] = mine0 ? r[0][e] : r[1][e];
-          }
+          for (int hx = 1; hx < NHW; ++hx)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rr[e] = hsel == hx ? r[hx][e] : rr[e];
 #pragma unroll
           for (int e = 0; e < 4; ++e) uf[kc][4 * s + e] = static_cast<T>(rr[e] * sgn);
         }
@@ -198,7 +211,8 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
     for (int kc = 0; kc < NK; ++kc) {
       const int ch = kc * 4 + lq;
       // rows past the item's tokens lie past the descriptor's range: zeros
-      u32x4 w = buf_load16(ru, ch < fchunks ? (tl * H + hh) * F * 2 + ch * 16 : 0x7fffffff);
+      u32x4 w = buf_load16(ru, ch < fchunks && hh < H ? (tl * H + hh) * F * 2 + ch * 16
+                                                       : 0x7fffffff);
       // waited for here, in the prologue, not inside the key loop where a
       // compiler vmcnt wait would also drain the LDS-DMA ring
       asm volatile("" : "+v"(w));
@@ -334,8 +348,6 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 #pragma unroll
     for (int t = 0; t < 8; ++t)
       bx[kc][t] = static_cast<T>(acc[2 * kc + (t >> 2)][t & 3] * inv);
-  const int h_first = (wave * 16) / TT;
-  const int nh = TT >= 16 ? 1 : 16 / TT;  // heads among the wave's rows
   constexpr int ND16 = DH / 16;
   typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
   for (int hx = 0; hx < nh; ++hx) {
@@ -379,12 +391,15 @@ void launch_fold(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
 
 template <typename T, int FP, int DH>
 void launch_fp(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
-  if (!a.fold)
-    launch_fold<T, FP, DH, 0>(a, wvt, st);
-  else if (kAbsorbRows / a.H < 16)  // 8 tokens per head: two heads per wave
-    launch_fold<T, FP, DH, 2>(a, wvt, st);
-  else
-    launch_fold<T, FP, DH, 1>(a, wvt, st);
+  if (!a.fold) return launch_fold<T, FP, DH, 0>(a, wvt, st);
+  if constexpr (DH <= 128) {
+    const int nhw = absorb_heads_per_wave(a.H);
+    if (nhw == 1) return launch_fold<T, FP, DH, 1>(a, wvt, st);
+    if constexpr (DH <= 64) {
+      if (nhw == 2) return launch_fold<T, FP, DH, 2>(a, wvt, st);
+    }
+    if constexpr (DH <= 32) return launch_fold<T, FP, DH, 4>(a, wvt, st);
+  }
 }
 
 template <typename T, int DH>
@@ -404,17 +419,43 @@ void launch_dh(const AbsorbArgs &a, const T *wvt, int FP, hipStream_t st) {
 
 using absorb::padded_f;
 
-// The matrix-core path takes H | 64 with at least 8 tokens per workgroup,
-// D_KV a multiple of 8 that pads (to 32) onto one of the compiled widths,
-// and D_H in {16, 32, 64, 128}.
+// The matrix-core path takes H <= 16 (floor(64/H) >= 4 tokens per item, so
+// a wave's 16 rows span at most 4 heads), D_KV a multiple of 8 up to 256
+// (padded onto one of the compiled widths), and D_H in {16, 32, 64, 128,
+// 256}.
 template <typename T>
 bool mfma_absorb_supported(int H, int F, int DH) {
-  const int FP = padded_f(F);
-  const bool f_ok = F % 8 == 0 && F <= kMaxF &&
-                    (FP == 64 || FP == 128 || FP == 192 || FP == 224 || FP == 256);
-  const bool h_ok = H >= 1 && H <= 8 && (kAbsorbRows % H) == 0;
-  const bool d_ok = DH == 16 || DH == 32 || DH == 64 || DH == 128;
+  const bool f_ok = F >= 8 && F % 8 == 0 && F <= kMaxF;
+  const bool h_ok = H >= 1 && H <= 16;
+  const bool d_ok = DH == 16 || DH == 32 || DH == 64 || DH == 128 || DH == 256;
   return f_ok && h_ok && d_ok;
+}
+
+// Most heads among the 16 rows of one forward wave (rows head-major,
+// floor(64/H) tokens per head).
+int absorb_heads_per_wave(int H) {
+  const int TT = kAbsorbRows / H;
+  int m = 0;
+  for (int w = 0; w < kFwdWaves; ++w) {
+    const int a = (16 * w) / TT;
+    if (a >= H) continue;
+    const int b = std::min(H - 1, (16 * w + 15) / TT);
+    m = std::max(m, b - a + 1);
+  }
+  return m;
+}
+
+// The folded forward forms u in the prologue: 2 * heads-per-wave * D_H/32
+// A-operand loads per 32-wide f chunk must fit its register batch (<= 8),
+// and above FP = 128 only the variants that keep three waves per SIMD
+// without spilling (at most two heads per wave, D_H <= 64; gfx950 register
+// counts of the compiled kernels) fold; other shapes read a projected u.
+bool mfma_absorb_fold_supported(int H, int F, int DH) {
+  if (!mfma_absorb_supported<bf16>(H, F, DH)) return false;
+  const int nhw = absorb_heads_per_wave(H);
+  const int nhw_t = nhw == 1 ? 1 : nhw == 2 ? 2 : 4;
+  if (nhw_t * (DH < 32 ? 1 : DH / 32) > 4) return false;
+  return padded_f(F) <= 128 || (nhw_t <= 2 && DH <= 64);
 }
 
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH) { return (int64_t)H * DH * padded_f(F); }
@@ -437,6 +478,7 @@ void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
     case 32: launch_dh<T, 32>(a, wvt, FP, st); break;
     case 64: launch_dh<T, 64>(a, wvt, FP, st); break;
     case 128: launch_dh<T, 128>(a, wvt, FP, st); break;
+    case 256: launch_dh<T, 256>(a, wvt, FP, st); break;
     default: break;
   }
 }

@@ -69,7 +69,16 @@ __device__ __forceinline__ void dma_block(const void *src, uint32_t bytes, int F
   }
 }
 
-inline int padded_f(int F) { return (F + 31) / 32 * 32; }
+// F padded up to the next width the matrix-core kernels are compiled for
+// (64, 128, 192, 224 or 256): the padding reads as zeros and every store is
+// bounded by F itself, so any F <= 256 with F % 8 == 0 runs on one of them.
+inline int padded_f(int F) {
+  const int f32 = (F + 31) / 32 * 32;
+  if (f32 <= 64) return 64;
+  if (f32 <= 128) return 128;
+  if (f32 <= 192) return 192;
+  return f32 <= 224 ? 224 : 256;
+}
 
 }  // namespace absorb
 }  // namespace vafa

@@ -685,7 +685,7 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
 static bool fold_supported(int64_t H, int64_t F, int64_t DH, int32_t dtype) {
   if (dtype != VAFA_BF16 && dtype != VAFA_F16) return false;
   if (H < 1 || H > 64 || F < 1 || F > 512 || DH < 1 || DH > 256) return false;
-  return mfma_absorb_supported<bf16>((int)H, (int)F, (int)DH);
+  return mfma_absorb_fold_supported((int)H, (int)F, (int)DH);
 }
 
 int vafa_absorb_fold_supported(int64_t H, int64_t D_KV, int64_t D_H, int32_t dtype) {

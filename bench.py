@@ -12,7 +12,8 @@ and max over its timed iterations, each bracketed by HIP events (the
 reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d16,d256,fused,copy,replay}
+       python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d16,d256,fused,copy,replay,
+                               absorb_shapes}
 """
 from __future__ import annotations
 
@@ -345,6 +346,30 @@ def bench_absorb_full(case, iters, unfused=False):
     return st, f_st
 
 
+def bench_absorb_shapes(iters):
+    """The absorb inner op on C4's lengths at the reference's other accepted
+    shapes (ta/interface.py:176, 200-201), each on its matrix-core path:
+    H = 16 and H = 6 (not dividing 64), D_H = 256, and D_KV = 512 (forward on
+    the FP = 512 kernel; its backward runs on the wave-per-row kernels and is
+    not timed here).  Returns {name: line}."""
+    import torch
+    from varlenabsorbflashattn_amd import workloads as W
+    c4 = W.config4(seed=0)
+    out = {}
+    for H, DH, F, bwd in ((16, 16, 256, True), (6, 32, 96, True), (8, 256, 256, True),
+                          (8, 32, 512, False)):
+        case = W.AbsorbCase(f"c4_lengths_H{H}_DH{DH}_F{F}", c4.q_lens, c4.k_lens, H, DH, F,
+                            torch.bfloat16)
+        st = bench_absorb(case, iters)
+        line = absorb_line(case, st)
+        if bwd:
+            b_st, _ = bench_absorb_bwd(case, iters)
+            line["fwd_bwd_ms"] = b_st
+        out[case.name] = line
+        log(case.name, st["mean"], line["GB/s"], line.get("fwd_bwd_ms", {}).get("mean"))
+    return out
+
+
 def absorb_line(case, st, full_st=None, unf_st=None):
     gbs = case.bytes_fwd() / (st["mean"] * 1e-3) / 1e9
     out = {"ms": st, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
@@ -533,6 +558,8 @@ def run_only(which, steps, warmup):
         u_st, uf_st = bench_absorb_full(case, max(steps, 1), unfused=True)
         return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st,
                 "unfused_fwd_bwd_ms": u_st, "unfused_fwd_ms": uf_st}
+    if which == "absorb_shapes":
+        return {"config": "absorb_shapes", **bench_absorb_shapes(max(steps, 3))}
     if which in ("c4b", "c4_fp32"):
         case = W.config4(seed=0)
         dt = torch.float32 if which == "c4_fp32" else None
@@ -554,7 +581,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c4full", "c5",
-                                       "d16", "d256", "fused", "copy", "replay"],
+                                       "d16", "d256", "fused", "copy", "replay",
+                                       "absorb_shapes"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -633,6 +661,9 @@ def main():
         rep = bench_replay(n2, 3, n_stage1=1, n_ta=1)
         secondary["replay_stage1_H4_D64"] = rep["stage1_H4_D64"][0]
         secondary["replay_ta_real_dq968_dkv216"] = rep["ta_real_dq968_dkv216"][0]
+        # absorb at the reference's other accepted shapes
+        for name, line in bench_absorb_shapes(n2).items():
+            secondary["absorb_" + name] = line
         # D=16 (16-bit: the D=32 kernels over zero-padded copies) at C2's shape
         c16 = W.VarlenCase("c2_lengths_H16_D16", case.q_lens, case.k_lens, 16, 16,
                            torch.bfloat16)

@@ -83,6 +83,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   constexpr int NK = FP / 32;   // 32-wide reduction chunks of S^T
   constexpr int NF = FP / 16;   // 16-row f tiles of aX^T
   constexpr int kPerWave = kBK / kFwdWaves;  // DMA instructions per wave per tile
+  constexpr int NBUF = S::kRing;
   constexpr int kPre = 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   // only tiles of the key range are fetched (a tile past it would land as
   // zeros and cost a tile's DMA instructions)
 #pragma unroll
-  for (int b = 0; b < kNBuf - 1; ++b)
+  for (int b = 0; b < NBUF - 1; ++b)
     if (b < nt) issue(k0 + b * kBK, b);
 
   // U^T fragments (B operand of S^T = X U^T): row `row`, f = 32*kc + 8*lq + t
@@ -231,18 +232,18 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
 
   const int a_off = l16 * S::XS + lq * 8;
   const int t_off = (4 * lq + (l16 >> 2)) * S::XS + 4 * (l16 & 3);
-  int buf = 0;  // j % kNBuf
+  int buf = 0;  // j % NBUF
   for (int j = 0; j < nt; ++j) {
     // tile j landed (tile j+1, if there is one, may still be in flight),
     // visible to all waves, and every wave is done with tile j-1 whose slot
     // is refilled next
-    static_assert(kNBuf == 3, "one tile in flight behind the current one");
-    if (j + 1 < nt)
-      wait_vmcnt<(kNBuf - 2) * kPerWave>();
+    // (3-deep ring: tile j+1 may stay in flight; 2-deep: none is)
+    if (NBUF == 3 && j + 1 < nt)
+      wait_vmcnt<(NBUF - 2) * kPerWave>();
     else
       wait_vmcnt<0>();
     __syncthreads();
-    if (j + kNBuf - 1 < nt) issue(k0 + (j + kNBuf - 1) * kBK, buf == 0 ? kNBuf - 1 : buf - 1);
+    if (j + NBUF - 1 < nt) issue(k0 + (j + NBUF - 1) * kBK, buf == 0 ? NBUF - 1 : buf - 1);
     const int kb = k0 + j * kBK;
     if (wave_active) {
       const lds_cptr<T> xa = as_lds(smem + buf * S::kTile + a_off);
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    buf = buf == kNBuf - 1 ? 0 : buf + 1;
+    buf = buf == NBUF - 1 ? 0 : buf + 1;
   }
   wait_vmcnt<0>();
 
@@ -410,6 +411,7 @@ void launch_dh(const AbsorbArgs &a, const T *wvt, int FP, hipStream_t st) {
     case 192: launch_fp<T, 192, DH>(a, wvt, st); break;
     case 224: launch_fp<T, 224, DH>(a, wvt, st); break;
     case 256: launch_fp<T, 256, DH>(a, wvt, st); break;
+    case 512: launch_fold<T, 512, DH, 0>(a, wvt, st); break;
     default: break;
   }
 }
@@ -429,6 +431,14 @@ bool mfma_absorb_supported(int H, int F, int DH) {
   const bool h_ok = H >= 1 && H <= 16;
   const bool d_ok = DH == 16 || DH == 32 || DH == 64 || DH == 128 || DH == 256;
   return f_ok && h_ok && d_ok;
+}
+
+// The forward kernel also takes 256 < D_KV <= 512 (FP = 512, 2-deep ring);
+// the backward kernels of those widths are the wave-per-row ones.
+template <typename T>
+bool mfma_absorb_fwd_supported(int H, int F, int DH) {
+  if (F > kMaxF && F <= kMaxFwdF && F % 8 == 0) return mfma_absorb_supported<T>(H, 8, DH);
+  return mfma_absorb_supported<T>(H, F, DH);
 }
 
 // Most heads among the 16 rows of one forward wave (rows head-major,
@@ -451,7 +461,7 @@ int absorb_heads_per_wave(int H) {
 // without spilling (at most two heads per wave, D_H <= 64; gfx950 register
 // counts of the compiled kernels) fold; other shapes read a projected u.
 bool mfma_absorb_fold_supported(int H, int F, int DH) {
-  if (!mfma_absorb_supported<bf16>(H, F, DH)) return false;
+  if (!mfma_absorb_supported<bf16>(H, F, DH)) return false;  // F <= 256
   const int nhw = absorb_heads_per_wave(H);
   const int nhw_t = nhw == 1 ? 1 : nhw == 2 ? 2 : 4;
   if (nhw_t * (DH < 32 ? 1 : DH / 32) > 4) return false;
@@ -485,6 +495,8 @@ void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
 
 template bool mfma_absorb_supported<bf16>(int, int, int);
 template bool mfma_absorb_supported<f16>(int, int, int);
+template bool mfma_absorb_fwd_supported<bf16>(int, int, int);
+template bool mfma_absorb_fwd_supported<f16>(int, int, int);
 template void launch_mfma_absorb_fwd<bf16>(const AbsorbArgs &, hipStream_t);
 template void launch_mfma_absorb_fwd<f16>(const AbsorbArgs &, hipStream_t);
 

@@ -10,6 +10,7 @@ namespace absorb {
 constexpr int kBK = 32;     // keys per LDS tile
 constexpr int kNBuf = 3;    // LDS ring depth
 constexpr int kMaxF = 256;  // D_KV handled by these kernels (padded to 32)
+constexpr int kMaxFwdF = 512;  // D_KV of the forward kernel (2-deep ring above kMaxF)
 
 // Row padding of the staged tiles (elements), by operand read pattern,
 // measured on gfx950 at 12 waves per CU with FP = 256: the 16x16x32 kernels
@@ -25,7 +26,10 @@ struct AbsSmem {
   static constexpr int CPR = FP / 8;                 // 16-byte chunks per X row
   static constexpr int XS = FP + Pad;                // padded row stride (elements)
   static constexpr int kTile = kBK * XS;             // elements per tile
-  static constexpr int kLoopBytes = kNBuf * kTile * 2;
+  // ring depth: 3 tiles, or 2 above 256 features (three 34 KB tiles would
+  // leave room for one workgroup per CU)
+  static constexpr int kRing = FP > kMaxF ? 2 : kNBuf;
+  static constexpr int kLoopBytes = kRing * kTile * 2;
   static constexpr int kEpiBytes = kAbsorbRows * XS * 2;
   static constexpr int kBytes = kLoopBytes > kEpiBytes ? kLoopBytes : kEpiBytes;
 };
@@ -70,14 +74,16 @@ __device__ __forceinline__ void dma_block(const void *src, uint32_t bytes, int F
 }
 
 // F padded up to the next width the matrix-core kernels are compiled for
-// (64, 128, 192, 224 or 256): the padding reads as zeros and every store is
-// bounded by F itself, so any F <= 256 with F % 8 == 0 runs on one of them.
+// (64, 128, 192, 224, 256; 512 for the forward): the padding reads as zeros
+// and every store is bounded by F itself, so any F % 8 == 0 up to the
+// largest width runs on one of them.
 inline int padded_f(int F) {
   const int f32 = (F + 31) / 32 * 32;
   if (f32 <= 64) return 64;
   if (f32 <= 128) return 128;
   if (f32 <= 192) return 192;
-  return f32 <= 224 ? 224 : 256;
+  if (f32 <= 224) return 224;
+  return f32 <= 256 ? 256 : 512;  // 512: the forward kernel only
 }
 
 }  // namespace absorb

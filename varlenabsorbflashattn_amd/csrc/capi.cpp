@@ -268,7 +268,7 @@ AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t D
 template <typename T>
 void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
-    if (mfma_absorb_supported<T>(a.H, a.F, a.DH)) {
+    if (mfma_absorb_fwd_supported<T>(a.H, a.F, a.DH)) {
       launch_mfma_absorb_fwd<T>(a, st);
     } else {
       launch_simt_absorb_fwd<T>(a, st);

@@ -123,6 +123,7 @@ template <typename T, int D> void launch_mfma_varlen_fkv(const VarlenArgs &, hip
 
 // absorb_mfma.hip (bf16 / f16)
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
+template <typename T> bool mfma_absorb_fwd_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
 bool mfma_absorb_fold_supported(int H, int F, int DH);
 int absorb_heads_per_wave(int H);

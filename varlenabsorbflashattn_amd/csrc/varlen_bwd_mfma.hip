@@ -68,7 +68,9 @@ template <int D>
 struct DkvSmem {
   static constexpr int kQs = GTile<D>::kElems;                // Q (or dO) rows
   static constexpr int kBufBytes = 2 * kQs * 2 + 2 * kRB * 4;  // Q, dO, LSE, delta
-  static constexpr int kBytes = 2 * kBufBytes;
+  // + the span of the last full-width DMA instruction past its tile (the
+  // instruction's masked lanes write nothing, the slack is never touched)
+  static constexpr int kBytes = 2 * kBufBytes + 1024;
 };
 
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
@@ -92,6 +94,48 @@ __device__ __forceinline__ void dma_rows(const T *src, int r0, int r_end, int H,
       lds_dma16(rs, base + GTile<D>::row(wave * RPW + n) * 2, voff);
     }
   }
+}
+
+// Query-block staging of the dK/dV and fused kernels: full width at D <= 64.
+template <typename T, int D, int NW>
+__device__ __forceinline__ void dma_block_rows(const T *src, int r0, int r_end, int H, int h,
+                                               uint32_t base, int wave, int lane);
+
+// The same block by full-width LDS-DMA: the instruction with index i writes
+// the tile's LDS bytes [1024 i, 1024 i + 1024), lane l the 16 bytes at
+// 1024 i + 16 l, so each lane fetches the (row, 16-byte chunk) that the GTile
+// layout places there; lanes whose position is row padding or past the tile
+// are masked off.  ceil(tile bytes / 1 KiB) instructions per block instead of
+// one per row (D = 64: 6 against 32 with 8 of 64 lanes active).  Measured on
+// the MI355X (A/B in one call): stage-1 replay (H=4, D=64) fwd+bwd 4.98 ->
+// 4.61 ms; C2's D=128 dK/dV kernel (8 waves, 256-key tiles) 0.93 -> 0.97 ms,
+// so D >= 128 keeps one instruction per row (16 or 32 active lanes).
+template <typename T, int D, int NW>
+__device__ __forceinline__ void dma_rows_wide(const T *src, int r0, int r_end, int H, int h,
+                                              uint32_t base, int wave, int lane) {
+  using L = GTile<D>;
+  constexpr int kInstr = (L::kElems / 8 + 63) / 64;
+  const int rows = uniform_clamp(r_end - r0, kRB);
+  const u32x4 rs = rsrc_words32(src + (int64_t)r0 * H * D, (uint32_t)(rows * H * D * 2));
+  for (int i = wave; i < kInstr; i += NW) {
+    const int e = (i * 64 + lane) * 8;       // element offset of this lane's 16 bytes
+    const int g = e / L::P2, w = e - g * L::P2;
+    const int j = w / L::P1, wr = w - j * L::P1;
+    if (e < L::kElems && j < 4 && wr < D) {
+      // rows at or past `rows` lie past the descriptor's range: zeros
+      const int voff = (((4 * g + j) * H + h) * D + wr) * 2;
+      lds_dma16(rs, base + i * 1024, voff);
+    }
+  }
+}
+
+template <typename T, int D, int NW>
+__device__ __forceinline__ void dma_block_rows(const T *src, int r0, int r_end, int H, int h,
+                                               uint32_t base, int wave, int lane) {
+  if constexpr (D <= 64)
+    dma_rows_wide<T, D, NW>(src, r0, r_end, H, h, base, wave, lane);
+  else
+    dma_rows<T, D, NW>(src, r0, r_end, H, h, base, wave, lane);
 }
 
 template <typename T, int D, int NW>
@@ -132,8 +176,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   // their products vanish whatever P is.
   auto issue = [&](int qb, int buf) {
     unsigned char *base = smem_raw + buf * S::kBufBytes;
-    dma_rows<T, D, NW>(q, qb, q1, H, h, lds_addr(base), wave, lane);
-    dma_rows<T, D, NW>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
+    dma_block_rows<T, D, NW>(q, qb, q1, H, h, lds_addr(base), wave, lane);
+    dma_block_rows<T, D, NW>(dout, qb, q1, H, h, lds_addr(base + S::kQs * 2), wave, lane);
     const float *vec = (wave & 1) ? delta : lse;
     const int rows = uniform_clamp(q1 - qb, kRB);
     const u32x4 rv = rsrc_words32(vec + (int64_t)qb * H + h, (uint32_t)(rows * H * 4));
@@ -390,8 +434,8 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
   // the query block (rows past q1 arrive as zeros: Q = dO = 0 there makes
   // all of their products vanish whatever P is); even waves DMA LSE, odd
   // waves delta
-  dma_rows<T, D, 4>(q, q0, q1, H, h, lds_addr(smem_raw + S::kQOff), wave, lane);
-  dma_rows<T, D, 4>(dout, q0, q1, H, h, lds_addr(smem_raw + S::kDoOff), wave, lane);
+  dma_block_rows<T, D, 4>(q, q0, q1, H, h, lds_addr(smem_raw + S::kQOff), wave, lane);
+  dma_block_rows<T, D, 4>(dout, q0, q1, H, h, lds_addr(smem_raw + S::kDoOff), wave, lane);
   {
     const float *vec = (wave & 1) ? delta : lse;
     const int rows = uniform_clamp(q1 - q0, kRB);

@@ -13,7 +13,7 @@ reference harness's statistics, benchmark_packed_varlen_flash_attn.py:295-313).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --only {c2,c2_128k,c3,c4,c4b,c4_fp32,c4full,c5,d16,d256,fused,copy,replay,
-                               absorb_shapes}
+                               absorb_shapes,fp32}
 """
 from __future__ import annotations
 
@@ -140,6 +140,32 @@ def bench_varlen_case(case, steps, warmup):
     fwd_st = timed(fwd, steps)
     torch.cuda.empty_cache()
     return step_st, fwd_st
+
+
+def bench_varlen_fp32(steps):
+    """fp32 varlen on the fp32 matrix cores (the reference's fp32 call,
+    fa/interface.py:163) on C2's lengths: fwd+bwd at H=16, D=64 (both
+    directions on v_mfma_f32_32x32x2_f32) and the forward at D=128 (its
+    backward runs on the wave-per-row kernels); plus configs[0] itself."""
+    import torch
+    from varlenabsorbflashattn_amd import workloads as W
+    c2 = W.config2(seed=0)
+    out = {}
+    case = W.VarlenCase("c2_lengths_H16_D64_fp32", c2.q_lens, c2.k_lens, 16, 64, torch.float32)
+    s_st, f_st = bench_varlen_case(case, steps, 3)
+    out[case.name] = varlen_line(case, s_st, f_st)
+    case = W.VarlenCase("c2_lengths_H16_D128_fp32", c2.q_lens, c2.k_lens, 16, 128, torch.float32)
+    _, _, fwd = _varlen_setup(case)
+    f_st = timed(fwd, steps)
+    torch.cuda.empty_cache()
+    out[case.name + "_fwd"] = {"fwd_ms": f_st,
+                               "fwd_TFLOP/s": case.flops_fwd / (f_st["mean"] * 1e-3) / 1e12}
+    c1 = W.config1(seed=0)
+    s_st, f_st = bench_varlen_case(c1, steps, 3)
+    out["configs0_fp32"] = varlen_line(c1, s_st, f_st)
+    for k_, v_ in out.items():
+        log(k_, v_["fwd_ms"]["mean"], v_.get("fwd_bwd_ms", {}).get("mean"))
+    return out
 
 
 def varlen_line(case, step_st, fwd_st):
@@ -558,6 +584,8 @@ def run_only(which, steps, warmup):
         u_st, uf_st = bench_absorb_full(case, max(steps, 1), unfused=True)
         return {"config": case.name + "_packed_target_attn", "fwd_bwd_ms": st, "fwd_ms": f_st,
                 "unfused_fwd_bwd_ms": u_st, "unfused_fwd_ms": uf_st}
+    if which == "fp32":
+        return {"config": "varlen_fp32", **bench_varlen_fp32(max(steps, 3))}
     if which == "absorb_shapes":
         return {"config": "absorb_shapes", **bench_absorb_shapes(max(steps, 3))}
     if which in ("c4b", "c4_fp32"):
@@ -582,7 +610,7 @@ def main():
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--only", choices=["c2", "c2_128k", "c3", "c4", "c4b", "c4_fp32", "c4full", "c5",
                                        "d16", "d256", "fused", "copy", "replay",
-                                       "absorb_shapes"],
+                                       "absorb_shapes", "fp32"],
                     help="run one configuration and print its own JSON line (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -661,6 +689,9 @@ def main():
         rep = bench_replay(n2, 3, n_stage1=1, n_ta=1)
         secondary["replay_stage1_H4_D64"] = rep["stage1_H4_D64"][0]
         secondary["replay_ta_real_dq968_dkv216"] = rep["ta_real_dq968_dkv216"][0]
+        # fp32 varlen on the fp32 matrix cores
+        for name, line in bench_varlen_fp32(n2).items():
+            secondary["varlen_" + name] = line
         # absorb at the reference's other accepted shapes
         for name, line in bench_absorb_shapes(n2).items():
             secondary["absorb_" + name] = line

@@ -112,6 +112,28 @@ def test_varlen_other_dtypes(device, dtype, D, lens):
         assert_close(n, a, r)
 
 
+F32_CASES = [
+    ("plain", [17, 64, 128, 200], [17, 64, 128, 200]),
+    ("split_k", [150, 20], [9000, 5000]),           # split items + LSE combine
+    ("wide_tiles", [300, 140, 9], [200, 260, 50]),  # 256-row query tiles (8 waves)
+    ("empty_and_tails", [0, 5, 33, 0], [3, 0, 70, 7]),
+    ("decode_split", [3, 16, 1], [3000, 1500, 1024]),
+]
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("name,q_lens,k_lens", F32_CASES, ids=[c[0] for c in F32_CASES])
+def test_varlen_fp32_matrix_cores(device, name, q_lens, k_lens, D):
+    """fp32 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32, D in {32, 64,
+    128}): forward and gradients against the fp64 oracle at the fp32 bound
+    (1e-4 / 1e-5), including split-K partials, 256-row tiles, empty segments
+    and key tails."""
+    print(f"[varlen f32 mfma] {name} q={q_lens} k={k_lens} D={D}", flush=True)
+    got, ref = run_case(q_lens, k_lens, 4, D, torch.float32, device)
+    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+        assert_close(n, a, r)
+
+
 def test_varlen_config1_fp32(device):
     """configs[0]: fp32, lens {17,64,128,200}, H=4, D=64 (N(0,1) inputs)."""
     got, ref = run_case([17, 64, 128, 200], [17, 64, 128, 200], 4, 64, torch.float32, device,

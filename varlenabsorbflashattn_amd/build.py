@@ -18,6 +18,7 @@ ROOT = os.path.dirname(HERE)
 LIB_NAME = "libvafa.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["plan.cpp", "capi.cpp", "simt.hip", "reduce.hip", "varlen_mfma.hip", "varlen_bwd_mfma.hip",
+           "varlen_f32.hip",
            "absorb_mfma.hip", "absorb_bwd_mfma.hip", "absorb_f32.hip",
            "absorb_project.hip"]
 ARCH = os.environ.get("VAFA_OFFLOAD_ARCH", "gfx950")

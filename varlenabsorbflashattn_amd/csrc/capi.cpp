@@ -136,6 +136,8 @@ void varlen_fwd_dispatch(const VarlenArgs &a, hipStream_t st) {
       case 256: launch_mfma_varlen_fwd<T, 256>(a, st); return;
       default: break;
     }
+  } else {
+    if (f32_varlen_mfma_d(a.D)) return launch_f32_varlen_fwd(a, st);
   }
   launch_simt_varlen_fwd<T>(a, st);
 }
@@ -183,7 +185,12 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
         if (a.D == 256) launch_mfma_varlen_dq<T, 256>(d, st);
       }
     }
-    if (!mfma) launch_simt_varlen_dq<T>(d, st);
+    if (!mfma) {
+      if (sizeof(T) == 4 && f32_varlen_bwd_mfma_d(a.D))
+        launch_f32_varlen_dq(d, st);
+      else
+        launch_simt_varlen_dq<T>(d, st);
+    }
     launch_sum_combine<T>(d.part_o, d.dq, d.comb_items, d.n_comb, d.H, d.D, d.comb_rows, st);
   } else {
     if constexpr (sizeof(T) == 2) {
@@ -200,16 +207,26 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
                               st);
       }
     }
-    if (!mfma) launch_simt_varlen_dkv<T>(a, st);
+    // fp32: the fp32 matrix-core kernels at D in {32, 64}, else wave-per-key
+    const bool f32m = sizeof(T) == 4 && f32_varlen_bwd_mfma_d(a.D);
+    if (!mfma) {
+      if (f32m)
+        launch_f32_varlen_dkv(a, st);
+      else
+        launch_simt_varlen_dkv<T>(a, st);
+    }
     if (!fq && a.n_fkv > 0) {
-      // fused-planned chunks without the fused kernel (fp32): the wave-per-key
-      // dK/dV kernel walks any key range ({k0, k1, q0, q1} leads both item
+      // fused-planned chunks without the fused kernel (fp32): both dK/dV
+      // kernels walk any key range ({k0, k1, q0, q1} leads both item
       // formats).  16-bit operands always take the fused kernel here: a plan
       // holds fused items only for D <= kFusedMaxD (check_varlen_tiles).
       VarlenArgs kv = a;
       kv.kv_items = a.fkv_items;
       kv.n_kv = a.n_fkv;
-      launch_simt_varlen_dkv<T>(kv, st);
+      if (f32m)
+        launch_f32_varlen_dkv(kv, st);
+      else
+        launch_simt_varlen_dkv<T>(kv, st);
     }
   }
 }

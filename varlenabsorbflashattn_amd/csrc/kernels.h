@@ -71,6 +71,13 @@ struct AbsorbArgs {
   float scale;
 };
 
+// varlen_f32.hip: fp32 varlen on fp32 matrix cores (D in {32, 64, 128})
+bool f32_varlen_mfma_d(int D);
+bool f32_varlen_bwd_mfma_d(int D);  // D in {32, 64}
+void launch_f32_varlen_fwd(const VarlenArgs &, hipStream_t);
+void launch_f32_varlen_dq(const VarlenArgs &, hipStream_t);
+void launch_f32_varlen_dkv(const VarlenArgs &, hipStream_t);
+
 // simt.hip
 template <typename T> void launch_simt_varlen_fwd(const VarlenArgs &, hipStream_t);
 template <typename T> void launch_simt_varlen_dq(const VarlenArgs &, hipStream_t);

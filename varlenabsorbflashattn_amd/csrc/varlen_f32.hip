@@ -1,0 +1,667 @@
+// Packed varlen FlashAttention in fp32 on gfx950 fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32, IEEE fp32 products; replaces fa/kernels.py:64-175
+// and 516-628 for fp32 inputs, fa/interface.py:163).
+//
+// Forward: one workgroup = NW waves (the plan's query tile / 32) of one head,
+// each wave owning 32 query rows; 32-key K/V tiles staged in LDS through
+// registers (the next tile's loads in flight under the current tile's
+// products, double-buffered LDS).  Per tile a wave forms
+//   S^T = K Q^T        (D/2 products, K rows as A, Q^T held in registers)
+//   O^T += V^T P^T     (D/2 products, V^T as A, P^T straight from S^T)
+// The reduction index of every product is relabelled so that each lane's
+// operands are 16-byte LDS reads:
+//   * S^T step s: lane half lh supplies d = lh*D/2 + s (A: K[key][d], B:
+//     Q[row][d]), four consecutive steps from one ds_read_b128 of a K row;
+//   * O^T step s: lane half lh supplies key 8*(s/4) + 4*lh + s%4 -- exactly
+//     the keys the S^T accumulator holds in its element s for that lane, so
+//     P^T needs no exchange, and V is staged transposed ([d][key]) so the
+//     four keys of s = 4j..4j+3 are one ds_read_b128.
+// The online softmax runs in the log2 domain (LSE = m + log2 l), as the
+// 16-bit kernels; split items write normalized fp32 partial rows.
+#include "common.h"
+#include "kernels.h"
+
+namespace vafa {
+
+namespace {
+
+constexpr int kF32BK = 32;  // keys per tile
+
+__device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+struct F32FwdSmem {
+  static constexpr int KS = D + 4;            // K row stride (floats): 16 rows hit 16 bank groups
+  static constexpr int VS = kF32BK + 4;       // V^T row stride (floats)
+  static constexpr int kK = kF32BK * KS;      // floats per K tile
+  static constexpr int kV = D * VS;           // floats per V^T tile
+  static constexpr int kBuf = kK + kV;
+  static constexpr int kBytes = 2 * kBuf * 4;  // double buffered
+};
+
+// Register stage of one 32-key K/V tile over NT threads: 16-byte chunks,
+// zeros past k_end.
+template <int D, int NT>
+struct F32Tile {
+  static constexpr int kChunks = kF32BK * D / 4;              // per tensor
+  static constexpr int kPer = (kChunks + NT - 1) / NT;        // per thread
+  f32x4 kc[kPer], vc[kPer];
+};
+
+template <int D, int NT>
+__device__ __forceinline__ void f32_load_tile(F32Tile<D, NT> &r, const float *k, const float *v,
+                                              int kbase, int k_end, int H, int h, int tid) {
+  using R = F32Tile<D, NT>;
+  constexpr int CPR = D / 4;
+  const int nk = k_end - kbase < kF32BK ? k_end - kbase : kF32BK;
+  const int64_t nbytes = (int64_t)nk * H * D * 4;
+  const rsrc_t rk = make_rsrc(k + (int64_t)kbase * H * D, nbytes);
+  const rsrc_t rv = make_rsrc(v + (int64_t)kbase * H * D, nbytes);
+#pragma unroll
+  for (int i = 0; i < R::kPer; ++i) {
+    const int ci = tid + NT * i;
+    const int key = ci < R::kChunks ? ci / CPR : kF32BK, dc = ci % CPR;  // kF32BK: zeros
+    const int off = (key * H + h) * D * 4 + dc * 16;
+    r.kc[i] = __builtin_bit_cast(f32x4, buf_load16(rk, off));
+    r.vc[i] = __builtin_bit_cast(f32x4, buf_load16(rv, off));
+  }
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void f32_store_tile(const F32Tile<D, NT> &r, float *ks, float *vts,
+                                               int tid) {
+  using R = F32Tile<D, NT>;
+  using S = F32FwdSmem<D>;
+  constexpr int CPR = D / 4;
+#pragma unroll
+  for (int i = 0; i < R::kPer; ++i) {
+    const int ci = tid + NT * i;
+    if (R::kChunks % NT == 0 || ci < R::kChunks) {
+      const int key = ci / CPR, d0 = (ci % CPR) * 4;
+      *reinterpret_cast<f32x4 *>(ks + key * S::KS + d0) = r.kc[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vts[(d0 + e) * S::VS + key] = r.vc[i][e];
+    }
+  }
+}
+
+// two waves per SIMD
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_fwd_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    float *__restrict__ o, float *__restrict__ lse, float *__restrict__ part_o,
+    float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, float c) {
+  using S = F32FwdSmem<D>;
+  constexpr int NT = 64 * NW;
+  constexpr int ND = D / 32;  // 32-row d tiles of O^T
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  float *smem = reinterpret_cast<float *>(smem_raw);
+
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int q0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int qrow = q0 + wave * 32 + l32;
+  const bool row_ok = qrow < q1;
+  const bool wave_active = q0 + wave * 32 < q1;
+
+  // Q^T operand: this lane's row at d = lh*D/2 + s, rows past q1 zero.  A
+  // negative scale is folded into Q (exact sign flips), so c > 0 below.
+  const float qsgn = c < 0.f ? -1.f : 1.f;
+  c = fabsf(c);
+  float qf[D / 2];
+  {
+    const rsrc_t rq = make_rsrc(q + ((int64_t)q0 * H + h) * D, (int64_t)(q1 - q0) * H * D * 4);
+    const int lr = wave * 32 + l32;
+#pragma unroll
+    for (int t = 0; t < D / 8; ++t) {
+      const f32x4 x = __builtin_bit_cast(f32x4, buf_load16(rq, (lr * H * D + lh * (D / 2) + 4 * t) * 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qf[4 * t + e] = x[e] * qsgn;
+    }
+  }
+  f32x16 acc[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  float m_run = kNegInf, l_part = 0.f;
+
+  const int nt = (k1 - k0 + kF32BK - 1) / kF32BK;
+  F32Tile<D, NT> regs;
+  if (nt > 0) {
+    f32_load_tile<D, NT>(regs, k, v, k0, k1, H, h, tid);
+    f32_store_tile<D, NT>(regs, smem, smem + S::kK, tid);
+  }
+  __syncthreads();
+  for (int j = 0; j < nt; ++j) {
+    const int kbase = k0 + j * kF32BK;
+    if (j + 1 < nt) f32_load_tile<D, NT>(regs, k, v, kbase + kF32BK, k1, H, h, tid);
+    const float *ks = smem + (j & 1) * S::kBuf;
+    const float *vts = ks + S::kK;
+    if (wave_active) {
+      // S^T = K Q^T
+      f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      const float *krow = ks + l32 * S::KS + lh * (D / 2);
+#pragma unroll
+      for (int t = 0; t < D / 8; ++t) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s = mma32f(a[e], qf[4 * t + e], s);
+      }
+      // element r: key kbase + 8*(r/4) + 4*lh + r%4 of this lane's row
+      if (kbase + kF32BK > k1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kbase + 8 * (r >> 2) + 4 * lh + (r & 3) >= k1) s[r] = kNegInf;
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      mx = max_xor32(mx) * c;
+      const float m_new = fmaxf(m_run, mx);
+      // a fully masked tile cannot occur (nt covers [k0, k1)), so m_new is finite
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = fast_exp2(__builtin_fmaf(s[r], c, -m_new));
+        l_part += p[r];
+      }
+      // O^T += V^T P^T: step s uses keys 8*(s/4) + 4*lh + s%4 (p[s] of this lane)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const float *vrow = vts + (dt * 32 + l32) * S::VS + 4 * lh;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 a = *reinterpret_cast<const f32x4 *>(vrow + 8 * jj);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[dt] = mma32f(a[e], p[4 * jj + e], acc[dt]);
+        }
+      }
+    }
+    // the other buffer held tile j-1, which every wave finished before the
+    // barrier that ended the previous trip
+    if (j + 1 < nt) {
+      float *nks = smem + ((j + 1) & 1) * S::kBuf;
+      f32_store_tile<D, NT>(regs, nks, nks + S::kK, tid);
+    }
+    __syncthreads();
+  }
+
+  if (!row_ok) return;
+  const float l = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float lse_v = l > 0.f ? m_run + fast_log2(l) : kNegInf;
+  // element r of tile dt: d = 32*dt + 8*(r/4) + 4*lh + r%4
+  float *orow = pbase < 0 ? o + ((int64_t)qrow * H + h) * D
+                          : part_o + ((int64_t)(pbase + (qrow - q0)) * H + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = acc[dt][g * 4 + e] * inv;
+      *reinterpret_cast<f32x4 *>(orow + dt * 32 + g * 8 + lh * 4) = w;
+    }
+  if (lh == 0) {
+    if (pbase < 0)
+      lse[(int64_t)qrow * H + h] = lse_v;
+    else
+      part_lse[(int64_t)(pbase + (qrow - q0)) * H + h] = lse_v;
+  }
+}
+
+template <int D, int NW>
+void launch_fwd_f32_nw(const VarlenArgs &a, hipStream_t st) {
+  const int smem = F32FwdSmem<D>::kBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_fwd_f32_kernel<D, NW>), smem);
+  hipLaunchKernelGGL((varlen_fwd_f32_kernel<D, NW>), dim3((unsigned)(a.n_items * a.H)),
+                     dim3(64 * NW), smem, st, (const float *)a.q, (const float *)a.k,
+                     (const float *)a.v, (float *)a.o, a.lse, a.part_o, a.part_lse, a.items, a.H,
+                     a.scale * kLog2e);
+}
+
+template <int D>
+void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
+  if (a.q_tile == kVarlenWideTile) return launch_fwd_f32_nw<D, 8>(a, st);
+  launch_fwd_f32_nw<D, 4>(a, st);
+}
+
+// ---------------------------------------------------------------------------
+// Backward (D in {32, 64}: at D = 128 the operands held in registers and the
+// accumulators would exceed the register file at two waves per SIMD).
+//
+// dQ, query-major over the forward's items (split items write scaled fp32
+// partial rows that the ordered sum adds): per 32-key tile
+//   S^T = K Q^T, dP^T = V dO^T      (K, V rows as A from LDS, Q^T, dO^T in
+//                                    registers, d relabelled as above)
+//   P^T = exp2(S^T c - LSE), dS^T = P^T (dP^T - delta)   (lane = query row)
+//   dQ^T += K^T dS^T                 (K^T staged transposed; step s takes the
+//                                    keys of S^T's element s, as the forward's PV)
+// ---------------------------------------------------------------------------
+template <int D>
+struct F32DqSmem {
+  static constexpr int KS = D + 4;
+  static constexpr int TS = kF32BK + 4;
+  static constexpr int kK = kF32BK * KS;       // K rows, then V rows
+  static constexpr int kKT = D * TS;           // K^T
+  static constexpr int kBuf = 2 * kK + kKT;
+  static constexpr int kBytes = 2 * kBuf * 4;
+};
+
+template <int D, int NT>
+__device__ __forceinline__ void f32_store_dq_tile(const F32Tile<D, NT> &r, float *ks, int tid) {
+  using R = F32Tile<D, NT>;
+  using S = F32DqSmem<D>;
+  constexpr int CPR = D / 4;
+  float *vs = ks + S::kK, *kts = ks + 2 * S::kK;
+#pragma unroll
+  for (int i = 0; i < R::kPer; ++i) {
+    const int ci = tid + NT * i;
+    if (R::kChunks % NT == 0 || ci < R::kChunks) {
+      const int key = ci / CPR, d0 = (ci % CPR) * 4;
+      *reinterpret_cast<f32x4 *>(ks + key * S::KS + d0) = r.kc[i];
+      *reinterpret_cast<f32x4 *>(vs + key * S::KS + d0) = r.vc[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kts[(d0 + e) * S::TS + key] = r.kc[i][e];
+    }
+  }
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_dq_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ part_dq,
+    const int32_t *__restrict__ items, int H, float c, float scale) {
+  using S = F32DqSmem<D>;
+  constexpr int NT = 64 * NW;
+  constexpr int ND = D / 32;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  float *smem = reinterpret_cast<float *>(smem_raw);
+
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int q0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int qrow = q0 + wave * 32 + l32;
+  const bool row_ok = qrow < q1;
+  const bool wave_active = q0 + wave * 32 < q1;
+
+  // Q^T and dO^T operands of this lane's row (zero past q1)
+  float qf[D / 2], gf[D / 2];
+  {
+    const int64_t nb = (int64_t)(q1 - q0) * H * D * 4;
+    const rsrc_t rq = make_rsrc(q + ((int64_t)q0 * H + h) * D, nb);
+    const rsrc_t rg = make_rsrc(dout + ((int64_t)q0 * H + h) * D, nb);
+    const int lr = wave * 32 + l32;
+#pragma unroll
+    for (int t = 0; t < D / 8; ++t) {
+      const int off = (lr * H * D + lh * (D / 2) + 4 * t) * 4;
+      const f32x4 x = __builtin_bit_cast(f32x4, buf_load16(rq, off));
+      const f32x4 y = __builtin_bit_cast(f32x4, buf_load16(rg, off));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qf[4 * t + e] = x[e];
+        gf[4 * t + e] = y[e];
+      }
+    }
+  }
+  const float L = row_ok ? lse[(int64_t)qrow * H + h] : 0.f;
+  const float dl = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+  f32x16 acc[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+  const int nt = (k1 - k0 + kF32BK - 1) / kF32BK;
+  F32Tile<D, NT> regs;
+  if (nt > 0) {
+    f32_load_tile<D, NT>(regs, k, v, k0, k1, H, h, tid);
+    f32_store_dq_tile<D, NT>(regs, smem, tid);
+  }
+  __syncthreads();
+  for (int j = 0; j < nt; ++j) {
+    const int kbase = k0 + j * kF32BK;
+    if (j + 1 < nt) f32_load_tile<D, NT>(regs, k, v, kbase + kF32BK, k1, H, h, tid);
+    const float *ks = smem + (j & 1) * S::kBuf;
+    const float *vs = ks + S::kK, *kts = ks + 2 * S::kK;
+    if (wave_active) {
+      f32x16 s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+      const float *krow = ks + l32 * S::KS + lh * (D / 2);
+      const float *vrow = vs + l32 * S::KS + lh * (D / 2);
+#pragma unroll
+      for (int t = 0; t < D / 8; ++t) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * t);
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(vrow + 4 * t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mma32f(a[e], qf[4 * t + e], s);
+          dp = mma32f(b[e], gf[4 * t + e], dp);
+        }
+      }
+      // element r: key kbase + 8*(r/4) + 4*lh + r%4; P = 0 past k1
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool kin = kbase + 8 * (r >> 2) + 4 * lh + (r & 3) < k1;
+        const float p = kin ? fast_exp2(__builtin_fmaf(s[r], c, -L)) : 0.f;
+        ds[r] = p * (dp[r] - dl);
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const float *trow = kts + (dt * 32 + l32) * S::TS + 4 * lh;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 a = *reinterpret_cast<const f32x4 *>(trow + 8 * jj);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[dt] = mma32f(a[e], ds[4 * jj + e], acc[dt]);
+        }
+      }
+    }
+    if (j + 1 < nt) {
+      float *nks = smem + ((j + 1) & 1) * S::kBuf;
+      f32_store_dq_tile<D, NT>(regs, nks, tid);
+    }
+    __syncthreads();
+  }
+  if (!row_ok) return;
+  // element r of tile dt: d = 32*dt + 8*(r/4) + 4*lh + r%4
+  float *orow = pbase < 0 ? dq + ((int64_t)qrow * H + h) * D
+                          : part_dq + ((int64_t)(pbase + (qrow - q0)) * H + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = acc[dt][g * 4 + e] * scale;
+      *reinterpret_cast<f32x4 *>(orow + dt * 32 + g * 8 + lh * 4) = w;
+    }
+}
+
+// dK/dV, key-major over the plan's key tiles (32 keys per wave): per 32-row
+// query block (Q, dO staged row-major and transposed, LSE and delta)
+//   S = Q K^T, dP = dO V^T           (Q, dO rows as A, K^T, V^T in registers:
+//                                    lane = key, d relabelled)
+//   P = exp2(S c - LSE), dS = P (dP - delta)   (element r: query row
+//                                    8*(r/4) + 4*lh + r%4 of the block)
+//   dV^T += dO^T P, dK^T += Q^T dS   (A from the transposed copies, B = P / dS
+//                                    element s: no exchange)
+template <int D>
+struct F32DkvSmem {
+  static constexpr int RS = D + 4;            // row-major Q / dO stride
+  static constexpr int TS = kF32BK + 4;       // transposed stride
+  static constexpr int kR = kF32BK * RS;
+  static constexpr int kT = D * TS;
+  static constexpr int kBuf = 2 * kR + 2 * kT + 2 * kF32BK;  // Q, dO, Q^T, dO^T, LSE, delta
+  static constexpr int kBytes = 2 * kBuf * 4;
+};
+
+template <int D, int NT>
+struct F32QBlk {
+  static constexpr int kChunks = kF32BK * D / 4;
+  static constexpr int kPer = (kChunks + NT - 1) / NT;
+  f32x4 qc[kPer], gc[kPer];
+  float lv, dv;
+};
+
+template <int D, int NT>
+__device__ __forceinline__ void f32_load_qblk(F32QBlk<D, NT> &r, const float *q,
+                                              const float *dout, const float *lse,
+                                              const float *delta, int qb, int q_end, int H,
+                                              int h, int tid) {
+  using R = F32QBlk<D, NT>;
+  constexpr int CPR = D / 4;
+  const int nq = q_end - qb < kF32BK ? q_end - qb : kF32BK;
+  const int64_t nbytes = (int64_t)nq * H * D * 4;
+  const rsrc_t rq = make_rsrc(q + (int64_t)qb * H * D, nbytes);
+  const rsrc_t rg = make_rsrc(dout + (int64_t)qb * H * D, nbytes);
+#pragma unroll
+  for (int i = 0; i < R::kPer; ++i) {
+    const int ci = tid + NT * i;
+    const int row = ci < R::kChunks ? ci / CPR : kF32BK, dc = ci % CPR;
+    const int off = (row * H + h) * D * 4 + dc * 16;
+    r.qc[i] = __builtin_bit_cast(f32x4, buf_load16(rq, off));
+    r.gc[i] = __builtin_bit_cast(f32x4, buf_load16(rg, off));
+  }
+  // rows past q_end: LSE = +inf makes P = 0 (their Q and dO are zero too)
+  const bool ok = tid < kF32BK && tid < nq;
+  r.lv = ok ? lse[(int64_t)(qb + tid) * H + h] : __builtin_inff();
+  r.dv = ok ? delta[(int64_t)(qb + tid) * H + h] : 0.f;
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void f32_store_qblk(const F32QBlk<D, NT> &r, float *base, int tid) {
+  using R = F32QBlk<D, NT>;
+  using S = F32DkvSmem<D>;
+  constexpr int CPR = D / 4;
+  float *qs = base, *gs = base + S::kR, *qt = base + 2 * S::kR, *gt = qt + S::kT;
+  float *ls = gt + S::kT;
+#pragma unroll
+  for (int i = 0; i < R::kPer; ++i) {
+    const int ci = tid + NT * i;
+    if (R::kChunks % NT == 0 || ci < R::kChunks) {
+      const int row = ci / CPR, d0 = (ci % CPR) * 4;
+      *reinterpret_cast<f32x4 *>(qs + row * S::RS + d0) = r.qc[i];
+      *reinterpret_cast<f32x4 *>(gs + row * S::RS + d0) = r.gc[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qt[(d0 + e) * S::TS + row] = r.qc[i][e];
+        gt[(d0 + e) * S::TS + row] = r.gc[i][e];
+      }
+    }
+  }
+  if (tid < kF32BK) {
+    ls[tid] = r.lv;
+    ls[kF32BK + tid] = r.dv;
+  }
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_dkv_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv,
+    const int32_t *__restrict__ items, int H, float c, float scale) {
+  using S = F32DkvSmem<D>;
+  constexpr int NT = 64 * NW;
+  constexpr int ND = D / 32;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  float *smem = reinterpret_cast<float *>(smem_raw);
+
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int kt0 = it.v[0], kt1 = it.v[1], q0 = it.v[2], q1 = it.v[3];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int nb = (q1 - q0 + kF32BK - 1) / kF32BK;
+  // an item holds one key tile of NW*32 keys, or (fused-planned chunks) a
+  // few: each sub-tile walks the query blocks on its own
+  for (int k0 = kt0; k0 < kt1; k0 += 32 * NW) {
+    const int k1 = kt1 - k0 < 32 * NW ? kt1 : k0 + 32 * NW;
+    const int key = k0 + wave * 32 + l32;
+    const bool key_ok = key < k1;
+    const bool wave_active = k0 + wave * 32 < k1;
+
+    // K^T and V^T operands of this lane's key (zero past k1)
+    float kf[D / 2], vf[D / 2];
+    {
+      const int64_t nbk = (int64_t)(k1 - k0) * H * D * 4;
+      const rsrc_t rk = make_rsrc(k + ((int64_t)k0 * H + h) * D, nbk);
+      const rsrc_t rv = make_rsrc(v + ((int64_t)k0 * H + h) * D, nbk);
+      const int lr = wave * 32 + l32;
+#pragma unroll
+      for (int t = 0; t < D / 8; ++t) {
+        const int off = (lr * H * D + lh * (D / 2) + 4 * t) * 4;
+        const f32x4 x = __builtin_bit_cast(f32x4, buf_load16(rk, off));
+        const f32x4 y = __builtin_bit_cast(f32x4, buf_load16(rv, off));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kf[4 * t + e] = x[e];
+          vf[4 * t + e] = y[e];
+        }
+      }
+    }
+    f32x16 adk[ND], adv[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) adk[i][r] = adv[i][r] = 0.f;
+
+    F32QBlk<D, NT> regs;
+    if (nb > 0) {
+      f32_load_qblk<D, NT>(regs, q, dout, lse, delta, q0, q1, H, h, tid);
+      f32_store_qblk<D, NT>(regs, smem, tid);
+    }
+    __syncthreads();
+    for (int j = 0; j < nb; ++j) {
+      const int qbase = q0 + j * kF32BK;
+      if (j + 1 < nb)
+        f32_load_qblk<D, NT>(regs, q, dout, lse, delta, qbase + kF32BK, q1, H, h, tid);
+      const float *base = smem + (j & 1) * S::kBuf;
+      const float *qs = base, *gs = base + S::kR, *qt = base + 2 * S::kR, *gt = qt + S::kT;
+      const float *ls = gt + S::kT;
+      if (wave_active) {
+        f32x16 s, dp;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+        const float *qrow = qs + l32 * S::RS + lh * (D / 2);
+        const float *grow = gs + l32 * S::RS + lh * (D / 2);
+#pragma unroll
+        for (int t = 0; t < D / 8; ++t) {
+          const f32x4 a = *reinterpret_cast<const f32x4 *>(qrow + 4 * t);
+          const f32x4 b = *reinterpret_cast<const f32x4 *>(grow + 4 * t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s = mma32f(a[e], kf[4 * t + e], s);
+            dp = mma32f(b[e], vf[4 * t + e], dp);
+          }
+        }
+        // element r: query row 8*(r/4) + 4*lh + r%4 of the block
+        float p[16], ds[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 L4 = *reinterpret_cast<const f32x4 *>(ls + 8 * g + 4 * lh);
+          const f32x4 D4 = *reinterpret_cast<const f32x4 *>(ls + kF32BK + 8 * g + 4 * lh);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            p[r] = fast_exp2(__builtin_fmaf(s[r], c, -L4[e]));
+            ds[r] = p[r] * (dp[r] - D4[e]);
+          }
+        }
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const float *gtr = gt + (dt * 32 + l32) * S::TS + 4 * lh;
+          const float *qtr = qt + (dt * 32 + l32) * S::TS + 4 * lh;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(gtr + 8 * jj);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(qtr + 8 * jj);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              adv[dt] = mma32f(a[e], p[4 * jj + e], adv[dt]);
+              adk[dt] = mma32f(b[e], ds[4 * jj + e], adk[dt]);
+            }
+          }
+        }
+      }
+      if (j + 1 < nb) f32_store_qblk<D, NT>(regs, smem + ((j + 1) & 1) * S::kBuf, tid);
+      __syncthreads();
+    }
+    if (key_ok) {
+      // element r of tile dt: d = 32*dt + 8*(r/4) + 4*lh + r%4 of this lane's key
+      float *krow = dk + ((int64_t)key * H + h) * D;
+      float *vrow = dv + ((int64_t)key * H + h) * D;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f32x4 wk, wv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wk[e] = adk[dt][g * 4 + e] * scale;
+            wv[e] = adv[dt][g * 4 + e];
+          }
+          *reinterpret_cast<f32x4 *>(krow + dt * 32 + g * 8 + lh * 4) = wk;
+          *reinterpret_cast<f32x4 *>(vrow + dt * 32 + g * 8 + lh * 4) = wv;
+        }
+    }
+  }
+}
+
+template <int D, int NW>
+void launch_dq_f32_nw(const VarlenArgs &a, hipStream_t st) {
+  const int smem = F32DqSmem<D>::kBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dq_f32_kernel<D, NW>), smem);
+  hipLaunchKernelGGL((varlen_dq_f32_kernel<D, NW>), dim3((unsigned)(a.n_items * a.H)),
+                     dim3(64 * NW), smem, st, (const float *)a.q, (const float *)a.k,
+                     (const float *)a.v, (const float *)a.dout, a.lse_in, a.delta,
+                     (float *)a.dq, a.part_o, a.items, a.H, a.scale * kLog2e, a.scale);
+}
+
+template <int D, int NW>
+void launch_dkv_f32_nw(const VarlenArgs &a, hipStream_t st) {
+  const int smem = F32DkvSmem<D>::kBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dkv_f32_kernel<D, NW>), smem);
+  hipLaunchKernelGGL((varlen_dkv_f32_kernel<D, NW>), dim3((unsigned)(a.n_kv * a.H)),
+                     dim3(64 * NW), smem, st, (const float *)a.q, (const float *)a.k,
+                     (const float *)a.v, (const float *)a.dout, a.lse_in, a.delta,
+                     (float *)a.dk, (float *)a.dv, a.kv_items, a.H, a.scale * kLog2e, a.scale);
+}
+
+}  // namespace
+
+bool f32_varlen_mfma_d(int D) { return D == 32 || D == 64 || D == 128; }
+bool f32_varlen_bwd_mfma_d(int D) { return D == 32 || D == 64; }
+
+void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
+  if (a.n_items == 0) return;
+  const bool wide = a.q_tile == kVarlenWideTile;
+  switch (a.D) {
+    case 32: wide ? launch_dq_f32_nw<32, 8>(a, st) : launch_dq_f32_nw<32, 4>(a, st); break;
+    case 64: wide ? launch_dq_f32_nw<64, 8>(a, st) : launch_dq_f32_nw<64, 4>(a, st); break;
+    default: break;
+  }
+}
+
+// Key tiles of the plan (kVarlenTile keys on 4 waves at D <= 64); the
+// kernel walks longer items (fused-planned chunks) in 128-key steps.
+void launch_f32_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
+  if (a.n_kv == 0) return;
+  switch (a.D) {
+    case 32: launch_dkv_f32_nw<32, 4>(a, st); break;
+    case 64: launch_dkv_f32_nw<64, 4>(a, st); break;
+    default: break;
+  }
+}
+
+void launch_f32_varlen_fwd(const VarlenArgs &a, hipStream_t st) {
+  if (a.n_items == 0) return;
+  switch (a.D) {
+    case 32: launch_fwd_f32_d<32>(a, st); break;
+    case 64: launch_fwd_f32_d<64>(a, st); break;
+    case 128: launch_fwd_f32_d<128>(a, st); break;
+    default: break;
+  }
+}
+
+}  // namespace vafa

@@ -144,17 +144,21 @@ def bench_varlen_case(case, steps, warmup):
 
 def bench_varlen_fp32(steps):
     """fp32 varlen on the fp32 matrix cores (the reference's fp32 call,
-    fa/interface.py:163) on C2's lengths: fwd+bwd at H=16, D=64 (both
-    directions on v_mfma_f32_32x32x2_f32) and the forward at D=128 (its
-    backward runs on the wave-per-row kernels); plus configs[0] itself."""
+    fa/interface.py:163) on C2's lengths: fwd+bwd at H=16 with D=16 (padded
+    to 32), 64 and 128 (both directions on v_mfma_f32_32x32x2_f32) and the
+    forward at H=8, D=256 (its backward runs on the wave-per-row kernels);
+    plus configs[0] itself."""
     import torch
     from varlenabsorbflashattn_amd import workloads as W
     c2 = W.config2(seed=0)
     out = {}
-    case = W.VarlenCase("c2_lengths_H16_D64_fp32", c2.q_lens, c2.k_lens, 16, 64, torch.float32)
-    s_st, f_st = bench_varlen_case(case, steps, 3)
-    out[case.name] = varlen_line(case, s_st, f_st)
-    case = W.VarlenCase("c2_lengths_H16_D128_fp32", c2.q_lens, c2.k_lens, 16, 128, torch.float32)
+    for D in (16, 64, 128):
+        case = W.VarlenCase(f"c2_lengths_H16_D{D}_fp32", c2.q_lens, c2.k_lens, 16, D,
+                            torch.float32)
+        s_st, f_st = bench_varlen_case(case, steps, 3)
+        out[case.name] = varlen_line(case, s_st, f_st)
+        torch.cuda.empty_cache()
+    case = W.VarlenCase("c2_lengths_H8_D256_fp32", c2.q_lens, c2.k_lens, 8, 256, torch.float32)
     _, _, fwd = _varlen_setup(case)
     f_st = timed(fwd, steps)
     torch.cuda.empty_cache()

@@ -148,8 +148,8 @@ VAFA_API int vafa_plan_absorb(const int64_t *cu_q, const int64_t *cu_k, int64_t 
 /* ======================================================================== */
 
 /* Workspace bytes needed by vafa_varlen_fwd / vafa_varlen_bwd.  For D=16 this
- * includes zero-padded D=32 copies of the operands: 16-bit D=16 calls run on
- * the D=32 matrix-core kernels over them (fp32 calls leave them unused). */
+ * includes zero-padded D=32 copies of the operands (sized for fp32 rows):
+ * D=16 calls run on the D=32 matrix-core kernels over them. */
 VAFA_API int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D);
 VAFA_API int64_t vafa_varlen_bwd_workspace(const vafa_plan_info *info, int64_t D);
 
@@ -178,7 +178,7 @@ VAFA_API int vafa_varlen_bwd(const void *q, const void *k, const void *v, const 
  * ends (it is part of the library's code object, so every GPU on which the
  * library is loaded holds it, whether or not this entry point is called):
  * same arguments otherwise, and the same kernels and results -- except for
- * 16-bit D=16, which vafa_varlen_fwd runs on the D=32 matrix-core kernels
+ * D=16, which vafa_varlen_fwd runs on the D=32 matrix-core kernels
  * over zero-padded copies in its workspace and this entry point runs on the
  * wave-per-row kernels (no room for the copies): both are within the parity
  * bound of the reference, not bit-identical.  The caller still passes inputs,

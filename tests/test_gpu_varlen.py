@@ -97,15 +97,15 @@ def test_varlen_bf16_parity(device, name, q_lens, k_lens, D):
 @pytest.mark.parametrize("lens", [
     ([17, 64, 128, 200], [17, 64, 128, 200]),
     # segments of <= 16 queries: the plan routes them to the fused key-major
-    # backward (chunks of up to 3 x 128 keys); fp32 runs those chunks on the
-    # wave-per-key dK/dV kernel and their dQ on the pass over forward items
+    # backward (chunks of up to 3 x 128 keys); fp32 runs those chunks on its
+    # dK/dV kernel (128-key steps) and their dQ on the pass over forward items
     ([16, 5, 1], [3000, 700, 64]),
 ], ids=["plain", "fused_planned"])
 @pytest.mark.parametrize("D", [64, 16])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
 def test_varlen_other_dtypes(device, dtype, D, lens):
-    """fp16 (matrix cores; at D=16 over zero-padded D=32 copies) and fp32 (the
-    wave-per-row kernels)."""
+    """fp16 and fp32 on the matrix cores (at D=16 over zero-padded D=32
+    copies)."""
     print(f"[varlen {dtype}] D={D} q={lens[0]} k={lens[1]}", flush=True)
     got, ref = run_case(lens[0], lens[1], 4, D, dtype, device)
     for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
@@ -121,13 +121,15 @@ F32_CASES = [
 ]
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("name,q_lens,k_lens", F32_CASES, ids=[c[0] for c in F32_CASES])
 def test_varlen_fp32_matrix_cores(device, name, q_lens, k_lens, D):
-    """fp32 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32, D in {32, 64,
-    128}): forward and gradients against the fp64 oracle at the fp32 bound
-    (1e-4 / 1e-5), including split-K partials, 256-row tiles, empty segments
-    and key tails."""
+    """fp32 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32): forward at D in
+    {32, 64, 128, 256}, gradients at D in {32, 64, 128} (D=256 gradients on the
+    wave-per-row kernels), D=16 over zero-padded D=32 copies; against the fp64
+    oracle at the fp32 bound (1e-4 / 1e-5), including split-K partials,
+    256-row tiles (walked as two 128-row halves in dQ at D=128), empty
+    segments and key tails."""
     print(f"[varlen f32 mfma] {name} q={q_lens} k={k_lens} D={D}", flush=True)
     got, ref = run_case(q_lens, k_lens, 4, D, torch.float32, device)
     for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):

@@ -93,12 +93,12 @@ struct VarlenWs {
   int64_t bytes = 0;
 };
 
-// D=16 with 16-bit operands runs on the D=32 matrix-core kernels over
-// zero-padded copies (the zero columns add exact zeros to every product; the
-// caller's scale is kept); fp32 D=16 stays on the wave-per-row kernels.
+// D=16 runs on the D=32 matrix-core kernels over zero-padded copies (the
+// zero columns add exact zeros to every product; the caller's scale is kept).
 inline bool pad_d16(int64_t D, int32_t dtype) {
-  return D == 16 && (dtype == VAFA_BF16 || dtype == VAFA_F16);
+  return D == 16 && (dtype == VAFA_BF16 || dtype == VAFA_F16 || dtype == VAFA_F32);
 }
+inline int elem_bytes(int32_t dtype) { return dtype == VAFA_F32 ? 4 : 2; }
 
 VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd, bool pad) {
   Carver c(ws);
@@ -110,7 +110,8 @@ VarlenWs carve_varlen(void *ws, const vafa_plan_info *info, int64_t D, bool bwd,
   if (!bwd) w.part_lse = c.take<float>(rows * 4);
   if (bwd) w.part_fq = c.take<float>(info->n_fpart_rows * info->H * Dc * 4);
   if (pad) {
-    const int64_t nq = info->T_q * info->H * 32 * 2, nk = info->T_k * info->H * 32 * 2;
+    // sized for fp32 rows: the workspace functions do not see the dtype
+    const int64_t nq = info->T_q * info->H * 32 * 4, nk = info->T_k * info->H * 32 * 4;
     w.pq = c.take<void>(nq);
     w.pk = c.take<void>(nk);
     w.pv = c.take<void>(nk);
@@ -149,9 +150,11 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
                         a.comb_rows, st);
 }
 
-// Backward stages.  Matrix-core kernels for D in {32, 64, 128, 256}; D=16
-// (below the 32-wide output tiles of the 32x32x16 products) and fp32 take the
-// wave-per-row kernels.  Segments the plan fuses (few queries, D <= 64) run
+// Backward stages.  16-bit matrix-core kernels for D in {32, 64, 128, 256},
+// fp32 ones for D in {32, 64, 128}; D=16 (below the 32-wide output tiles)
+// reaches them padded to 32 from vafa_varlen_bwd, and fp32 D=256 and the
+// stage entry points' D=16 take the wave-per-row kernels.  Segments the plan
+// fuses (few queries, D <= 64) run
 // dQ/dK/dV in the fused key-major kernel, whose dQ partials are summed in
 // order; without matrix cores their key tiles go to the plain dK/dV kernel
 // and their dQ to the dQ pass over every forward item.
@@ -503,7 +506,7 @@ extern "C" {
 const char *vafa_version(void) { return "vafa 0.1.0 gfx950"; }
 
 // The workspace functions do not see the dtype: for D=16 they include the
-// padded copies, which only 16-bit calls use.
+// padded copies, sized for fp32 rows.
 int64_t vafa_varlen_fwd_workspace(const vafa_plan_info *info, int64_t D) {
   if (check_info(info, 1)) return -1;
   return carve_varlen(nullptr, info, D, false, D == 16).bytes;
@@ -538,14 +541,15 @@ static int varlen_fwd_impl(const void *q, const void *k, const void *v, void *o,
   a.T_q = info->T_q; a.H = (int)info->H; a.D = (int)D; a.scale = scale;
   a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
   a.xcd_heads = (int)info->xcd_heads;
+  const int eb = elem_bytes(dtype);
   if (pad) {
-    launch_pad16(q, w.pq, info->T_q * info->H, st);
-    launch_pad16(k, w.pk, info->T_k * info->H, st);
-    launch_pad16(v, w.pv, info->T_k * info->H, st);
+    launch_pad16(q, w.pq, info->T_q * info->H, eb, st);
+    launch_pad16(k, w.pk, info->T_k * info->H, eb, st);
+    launch_pad16(v, w.pv, info->T_k * info->H, eb, st);
     a.q = w.pq; a.k = w.pk; a.v = w.pv; a.o = w.po; a.D = 32;
   }
   if (int rc = by_dtype<VFwd>(dtype, a, st)) return rc;
-  if (pad) launch_unpad16(w.po, o, info->T_q * info->H, st);
+  if (pad) launch_unpad16(w.po, o, info->T_q * info->H, eb, st);
   return check_launch("vafa_varlen_fwd");
 }
 
@@ -616,22 +620,23 @@ static int varlen_bwd_entry(int32_t stage, const void *q, const void *k, const v
   a.q_tile = (int)info->q_tile; a.k_tile = (int)info->k_tile;
   a.xcd_heads = (int)info->xcd_heads;
   a.stage = stage;
+  const int eb = elem_bytes(dtype);
   if (pad) {
     const int64_t rq = info->T_q * info->H, rk = info->T_k * info->H;
-    launch_pad16(q, w.pq, rq, st);
-    launch_pad16(k, w.pk, rk, st);
-    launch_pad16(v, w.pv, rk, st);
-    launch_pad16(o, w.po, rq, st);
-    launch_pad16(dout, w.pdo, rq, st);
+    launch_pad16(q, w.pq, rq, eb, st);
+    launch_pad16(k, w.pk, rk, eb, st);
+    launch_pad16(v, w.pv, rk, eb, st);
+    launch_pad16(o, w.po, rq, eb, st);
+    launch_pad16(dout, w.pdo, rq, eb, st);
     a.q = w.pq; a.k = w.pk; a.v = w.pv; a.o_in = w.po; a.dout = w.pdo;
     a.dq = w.pdq; a.dk = w.pdk; a.dv = w.pdv; a.D = 32;
   }
   const int rc = stage < 0 ? by_dtype<VBwd>(dtype, a, st) : by_dtype<VBwdStage>(dtype, a, st);
   if (rc) return rc;
   if (pad) {
-    launch_unpad16(w.pdq, dq, info->T_q * info->H, st);
-    launch_unpad16(w.pdk, dk, info->T_k * info->H, st);
-    launch_unpad16(w.pdv, dv, info->T_k * info->H, st);
+    launch_unpad16(w.pdq, dq, info->T_q * info->H, eb, st);
+    launch_unpad16(w.pdk, dk, info->T_k * info->H, eb, st);
+    launch_unpad16(w.pdv, dv, info->T_k * info->H, eb, st);
   }
   return check_launch("vafa_varlen_bwd");
 }

@@ -71,9 +71,9 @@ struct AbsorbArgs {
   float scale;
 };
 
-// varlen_f32.hip: fp32 varlen on fp32 matrix cores (D in {32, 64, 128})
-bool f32_varlen_mfma_d(int D);
-bool f32_varlen_bwd_mfma_d(int D);  // D in {32, 64}
+// varlen_f32.hip: fp32 varlen on fp32 matrix cores
+bool f32_varlen_mfma_d(int D);      // D in {32, 64, 128, 256}
+bool f32_varlen_bwd_mfma_d(int D);  // D in {32, 64, 128}
 void launch_f32_varlen_fwd(const VarlenArgs &, hipStream_t);
 void launch_f32_varlen_dq(const VarlenArgs &, hipStream_t);
 void launch_f32_varlen_dkv(const VarlenArgs &, hipStream_t);
@@ -111,9 +111,10 @@ void launch_absorb_dwv(const AbsorbArgs &, hipStream_t);
 template <typename TA, typename T>
 void launch_wgrad(const void *a, const void *b, float *part, void *out, int64_t T_q,
                   int64_t tchunk, int64_t n_chunks, int G, int F, int DH, hipStream_t);
-// 16-bit rows [rows, 16] -> zero-padded [rows, 32], and the first 16 columns back
-void launch_pad16(const void *src, void *dst, int64_t rows, hipStream_t);
-void launch_unpad16(const void *src, void *dst, int64_t rows, hipStream_t);
+// rows [rows, 16] -> zero-padded [rows, 32], and the first 16 columns back
+// (elem_bytes: 2 for 16-bit elements, 4 for fp32)
+void launch_pad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t);
+void launch_unpad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t);
 // out[o] = sum_c part[c * n_out + o] in chunk order, rounded to T
 template <typename T>
 void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chunks, hipStream_t);

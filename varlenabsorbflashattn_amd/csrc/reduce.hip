@@ -434,26 +434,28 @@ __global__ __launch_bounds__(256) void absorb_dwv_sum_kernel(const float *__rest
 }
 
 // [rows, 16] -> [rows, 32] with zero columns 16..31, and back: D=16 runs on
-// the D=32 matrix-core kernels (16-bit elements, 16-byte chunks).
-__global__ __launch_bounds__(256) void pad16_kernel(const uint16_t *__restrict__ src,
-                                                    uint16_t *__restrict__ dst, int64_t rows) {
+// the D=32 matrix-core kernels.  A row of 16 elements is cpr 16-byte chunks
+// (2 for 16-bit elements, 4 for fp32); its padded copy is 2 * cpr chunks.
+__global__ __launch_bounds__(256) void pad16_kernel(const u32x4 *__restrict__ src,
+                                                    u32x4 *__restrict__ dst, int64_t rows,
+                                                    int cpr) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= rows * 4) return;
-  const int64_t r = i >> 2;
-  const int c = (int)(i & 3);
+  if (i >= rows * 2 * cpr) return;
+  const int64_t r = i / (2 * cpr);
+  const int c = (int)(i % (2 * cpr));
   u32x4 v = {0u, 0u, 0u, 0u};
-  if (c < 2) v = *reinterpret_cast<const u32x4 *>(src + r * 16 + c * 8);
-  *reinterpret_cast<u32x4 *>(dst + r * 32 + c * 8) = v;
+  if (c < cpr) v = src[r * cpr + c];
+  dst[r * 2 * cpr + c] = v;
 }
 
-__global__ __launch_bounds__(256) void unpad16_kernel(const uint16_t *__restrict__ src,
-                                                      uint16_t *__restrict__ dst, int64_t rows) {
+__global__ __launch_bounds__(256) void unpad16_kernel(const u32x4 *__restrict__ src,
+                                                      u32x4 *__restrict__ dst, int64_t rows,
+                                                      int cpr) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= rows * 2) return;
-  const int64_t r = i >> 1;
-  const int c = (int)(i & 1);
-  *reinterpret_cast<u32x4 *>(dst + r * 16 + c * 8) =
-      *reinterpret_cast<const u32x4 *>(src + r * 32 + c * 8);
+  if (i >= rows * cpr) return;
+  const int64_t r = i / cpr;
+  const int c = (int)(i % cpr);
+  dst[r * cpr + c] = src[r * 2 * cpr + c];
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -554,16 +556,18 @@ void launch_absorb_dwv(const AbsorbArgs &a, hipStream_t st) {
                          a.DH, st);
 }
 
-void launch_pad16(const void *src, void *dst, int64_t rows, hipStream_t st) {
+void launch_pad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t st) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(pad16_kernel, dim3(blocks_for(rows * 4)), dim3(256), 0, st,
-                     (const uint16_t *)src, (uint16_t *)dst, rows);
+  const int cpr = elem_bytes;  // 16 elements = elem_bytes 16-byte chunks
+  hipLaunchKernelGGL(pad16_kernel, dim3(blocks_for(rows * 2 * cpr)), dim3(256), 0, st,
+                     (const u32x4 *)src, (u32x4 *)dst, rows, cpr);
 }
 
-void launch_unpad16(const void *src, void *dst, int64_t rows, hipStream_t st) {
+void launch_unpad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t st) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(unpad16_kernel, dim3(blocks_for(rows * 2)), dim3(256), 0, st,
-                     (const uint16_t *)src, (uint16_t *)dst, rows);
+  const int cpr = elem_bytes;
+  hipLaunchKernelGGL(unpad16_kernel, dim3(blocks_for(rows * cpr)), dim3(256), 0, st,
+                     (const u32x4 *)src, (u32x4 *)dst, rows, cpr);
 }
 
 #define VAFA_INST(T)                                                                        \

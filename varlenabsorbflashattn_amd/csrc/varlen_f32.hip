@@ -87,9 +87,10 @@ __device__ __forceinline__ void f32_store_tile(const F32Tile<D, NT> &r, float *k
   }
 }
 
-// two waves per SIMD
+// two waves per SIMD (one at D = 256, whose Q^T operands and accumulators
+// take 256 registers)
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_fwd_f32_kernel(
+__global__ __launch_bounds__(64 * NW, NW == 8 || D >= 256 ? 1 : 2) void varlen_fwd_f32_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     float *__restrict__ o, float *__restrict__ lse, float *__restrict__ part_o,
     float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, float c) {
@@ -234,15 +235,19 @@ void launch_fwd_f32_nw(const VarlenArgs &a, hipStream_t st) {
                      a.scale * kLog2e);
 }
 
+// the planner gives 256-row query tiles only to D <= 128
 template <int D>
 void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
-  if (a.q_tile == kVarlenWideTile) return launch_fwd_f32_nw<D, 8>(a, st);
+  if constexpr (D <= 128) {
+    if (a.q_tile == kVarlenWideTile) return launch_fwd_f32_nw<D, 8>(a, st);
+  }
   launch_fwd_f32_nw<D, 4>(a, st);
 }
 
 // ---------------------------------------------------------------------------
-// Backward (D in {32, 64}: at D = 128 the operands held in registers and the
-// accumulators would exceed the register file at two waves per SIMD).
+// Backward (D in {32, 64, 128}).  At D = 128 the operands held in registers
+// and the accumulators take more than half the register file, so those
+// workgroups run one wave per SIMD; at D = 256 they would not fit at all.
 //
 // dQ, query-major over the forward's items (split items write scaled fp32
 // partial rows that the ordered sum adds): per 32-key tile
@@ -251,6 +256,8 @@ void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
 //   P^T = exp2(S^T c - LSE), dS^T = P^T (dP^T - delta)   (lane = query row)
 //   dQ^T += K^T dS^T                 (K^T staged transposed; step s takes the
 //                                    keys of S^T's element s, as the forward's PV)
+// An item's rows are walked 32*NW at a time, so a 256-row item also runs on
+// four waves (D = 128) by streaming its key range twice.
 // ---------------------------------------------------------------------------
 template <int D>
 struct F32DqSmem {
@@ -282,7 +289,7 @@ __device__ __forceinline__ void f32_store_dq_tile(const F32Tile<D, NT> &r, float
 }
 
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_dq_f32_kernel(
+__global__ __launch_bounds__(64 * NW, NW == 8 || D >= 128 ? 1 : 2) void varlen_dq_f32_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ part_dq,
@@ -295,106 +302,110 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_dq_f32_kernel
 
   const int item = blockIdx.x / H, h = blockIdx.x % H;
   const PlanItem it = load_item(items, item);
-  const int q0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
+  const int iq0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, lh = lane >> 5;
-  const int qrow = q0 + wave * 32 + l32;
-  const bool row_ok = qrow < q1;
-  const bool wave_active = q0 + wave * 32 < q1;
-
-  // Q^T and dO^T operands of this lane's row (zero past q1)
-  float qf[D / 2], gf[D / 2];
-  {
-    const int64_t nb = (int64_t)(q1 - q0) * H * D * 4;
-    const rsrc_t rq = make_rsrc(q + ((int64_t)q0 * H + h) * D, nb);
-    const rsrc_t rg = make_rsrc(dout + ((int64_t)q0 * H + h) * D, nb);
-    const int lr = wave * 32 + l32;
-#pragma unroll
-    for (int t = 0; t < D / 8; ++t) {
-      const int off = (lr * H * D + lh * (D / 2) + 4 * t) * 4;
-      const f32x4 x = __builtin_bit_cast(f32x4, buf_load16(rq, off));
-      const f32x4 y = __builtin_bit_cast(f32x4, buf_load16(rg, off));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qf[4 * t + e] = x[e];
-        gf[4 * t + e] = y[e];
-      }
-    }
-  }
-  const float L = row_ok ? lse[(int64_t)qrow * H + h] : 0.f;
-  const float dl = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
-  f32x16 acc[ND];
-#pragma unroll
-  for (int i = 0; i < ND; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  const int nt = (k1 - k0 + kF32BK - 1) / kF32BK;
-  F32Tile<D, NT> regs;
-  if (nt > 0) {
-    f32_load_tile<D, NT>(regs, k, v, k0, k1, H, h, tid);
-    f32_store_dq_tile<D, NT>(regs, smem, tid);
-  }
-  __syncthreads();
-  for (int j = 0; j < nt; ++j) {
-    const int kbase = k0 + j * kF32BK;
-    if (j + 1 < nt) f32_load_tile<D, NT>(regs, k, v, kbase + kF32BK, k1, H, h, tid);
-    const float *ks = smem + (j & 1) * S::kBuf;
-    const float *vs = ks + S::kK, *kts = ks + 2 * S::kK;
-    if (wave_active) {
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-      const float *krow = ks + l32 * S::KS + lh * (D / 2);
-      const float *vrow = vs + l32 * S::KS + lh * (D / 2);
+  for (int q0 = iq0; q0 < q1; q0 += 32 * NW) {
+    const int qrow = q0 + wave * 32 + l32;
+    const bool row_ok = qrow < q1;
+    const bool wave_active = q0 + wave * 32 < q1;
+    // Q^T and dO^T operands of this lane's row (zero past q1)
+    float qf[D / 2], gf[D / 2];
+    {
+      const int64_t nb = (int64_t)(q1 - q0) * H * D * 4;
+      const rsrc_t rq = make_rsrc(q + ((int64_t)q0 * H + h) * D, nb);
+      const rsrc_t rg = make_rsrc(dout + ((int64_t)q0 * H + h) * D, nb);
+      const int lr = wave * 32 + l32;
 #pragma unroll
       for (int t = 0; t < D / 8; ++t) {
-        const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * t);
-        const f32x4 b = *reinterpret_cast<const f32x4 *>(vrow + 4 * t);
+        const int off = (lr * H * D + lh * (D / 2) + 4 * t) * 4;
+        const f32x4 x = __builtin_bit_cast(f32x4, buf_load16(rq, off));
+        const f32x4 y = __builtin_bit_cast(f32x4, buf_load16(rg, off));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          s = mma32f(a[e], qf[4 * t + e], s);
-          dp = mma32f(b[e], gf[4 * t + e], dp);
-        }
-      }
-      // element r: key kbase + 8*(r/4) + 4*lh + r%4; P = 0 past k1
-      float ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool kin = kbase + 8 * (r >> 2) + 4 * lh + (r & 3) < k1;
-        const float p = kin ? fast_exp2(__builtin_fmaf(s[r], c, -L)) : 0.f;
-        ds[r] = p * (dp[r] - dl);
-      }
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const float *trow = kts + (dt * 32 + l32) * S::TS + 4 * lh;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 a = *reinterpret_cast<const f32x4 *>(trow + 8 * jj);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[dt] = mma32f(a[e], ds[4 * jj + e], acc[dt]);
+          qf[4 * t + e] = x[e];
+          gf[4 * t + e] = y[e];
         }
       }
     }
-    if (j + 1 < nt) {
-      float *nks = smem + ((j + 1) & 1) * S::kBuf;
-      f32_store_dq_tile<D, NT>(regs, nks, tid);
+    const float L = row_ok ? lse[(int64_t)qrow * H + h] : 0.f;
+    const float dl = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+    f32x16 acc[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+    const int nt = (k1 - k0 + kF32BK - 1) / kF32BK;
+    F32Tile<D, NT> regs;
+    if (nt > 0) {
+      f32_load_tile<D, NT>(regs, k, v, k0, k1, H, h, tid);
+      f32_store_dq_tile<D, NT>(regs, smem, tid);
     }
     __syncthreads();
-  }
-  if (!row_ok) return;
-  // element r of tile dt: d = 32*dt + 8*(r/4) + 4*lh + r%4
-  float *orow = pbase < 0 ? dq + ((int64_t)qrow * H + h) * D
-                          : part_dq + ((int64_t)(pbase + (qrow - q0)) * H + h) * D;
+    for (int j = 0; j < nt; ++j) {
+      const int kbase = k0 + j * kF32BK;
+      if (j + 1 < nt) f32_load_tile<D, NT>(regs, k, v, kbase + kF32BK, k1, H, h, tid);
+      const float *ks = smem + (j & 1) * S::kBuf;
+      const float *vs = ks + S::kK, *kts = ks + 2 * S::kK;
+      if (wave_active) {
+        f32x16 s, dp;
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt)
+        for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+        const float *krow = ks + l32 * S::KS + lh * (D / 2);
+        const float *vrow = vs + l32 * S::KS + lh * (D / 2);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f32x4 w;
+        for (int t = 0; t < D / 8; ++t) {
+          const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * t);
+          const f32x4 b = *reinterpret_cast<const f32x4 *>(vrow + 4 * t);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = acc[dt][g * 4 + e] * scale;
-      *reinterpret_cast<f32x4 *>(orow + dt * 32 + g * 8 + lh * 4) = w;
+          for (int e = 0; e < 4; ++e) {
+            s = mma32f(a[e], qf[4 * t + e], s);
+            dp = mma32f(b[e], gf[4 * t + e], dp);
+          }
+        }
+        // element r: key kbase + 8*(r/4) + 4*lh + r%4; P = 0 past k1
+        float ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool kin = kbase + 8 * (r >> 2) + 4 * lh + (r & 3) < k1;
+          const float p = kin ? fast_exp2(__builtin_fmaf(s[r], c, -L)) : 0.f;
+          ds[r] = p * (dp[r] - dl);
+        }
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const float *trow = kts + (dt * 32 + l32) * S::TS + 4 * lh;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(trow + 8 * jj);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[dt] = mma32f(a[e], ds[4 * jj + e], acc[dt]);
+          }
+        }
+      }
+      if (j + 1 < nt) {
+        float *nks = smem + ((j + 1) & 1) * S::kBuf;
+        f32_store_dq_tile<D, NT>(regs, nks, tid);
+      }
+      __syncthreads();
     }
+    if (row_ok) {
+      // element r of tile dt: d = 32*dt + 8*(r/4) + 4*lh + r%4
+      float *orow = pbase < 0 ? dq + ((int64_t)qrow * H + h) * D
+                              : part_dq + ((int64_t)(pbase + (qrow - iq0)) * H + h) * D;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = acc[dt][g * 4 + e] * scale;
+          *reinterpret_cast<f32x4 *>(orow + dt * 32 + g * 8 + lh * 4) = w;
+        }
+    }
+    // the next sub-tile's first LDS store follows the last barrier above,
+    // after which no wave reads LDS
+  }
 }
 
 // dK/dV, key-major over the plan's key tiles (32 keys per wave): per 32-row
@@ -476,7 +487,7 @@ __device__ __forceinline__ void f32_store_qblk(const F32QBlk<D, NT> &r, float *b
 }
 
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void varlen_dkv_f32_kernel(
+__global__ __launch_bounds__(64 * NW, NW == 8 || D >= 128 ? 1 : 2) void varlen_dkv_f32_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv,
@@ -630,8 +641,8 @@ void launch_dkv_f32_nw(const VarlenArgs &a, hipStream_t st) {
 
 }  // namespace
 
-bool f32_varlen_mfma_d(int D) { return D == 32 || D == 64 || D == 128; }
-bool f32_varlen_bwd_mfma_d(int D) { return D == 32 || D == 64; }
+bool f32_varlen_mfma_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+bool f32_varlen_bwd_mfma_d(int D) { return D == 32 || D == 64 || D == 128; }
 
 void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
   if (a.n_items == 0) return;
@@ -639,17 +650,19 @@ void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
   switch (a.D) {
     case 32: wide ? launch_dq_f32_nw<32, 8>(a, st) : launch_dq_f32_nw<32, 4>(a, st); break;
     case 64: wide ? launch_dq_f32_nw<64, 8>(a, st) : launch_dq_f32_nw<64, 4>(a, st); break;
+    case 128: launch_dq_f32_nw<128, 4>(a, st); break;  // walks 256-row items in halves
     default: break;
   }
 }
 
-// Key tiles of the plan (kVarlenTile keys on 4 waves at D <= 64); the
-// kernel walks longer items (fused-planned chunks) in 128-key steps.
+// Key tiles of the plan on 4 waves; the kernel walks longer items (256-key
+// tiles at D = 128, fused-planned chunks at D <= 64) in 128-key steps.
 void launch_f32_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
   switch (a.D) {
     case 32: launch_dkv_f32_nw<32, 4>(a, st); break;
     case 64: launch_dkv_f32_nw<64, 4>(a, st); break;
+    case 128: launch_dkv_f32_nw<128, 4>(a, st); break;
     default: break;
   }
 }
@@ -660,6 +673,7 @@ void launch_f32_varlen_fwd(const VarlenArgs &a, hipStream_t st) {
     case 32: launch_fwd_f32_d<32>(a, st); break;
     case 64: launch_fwd_f32_d<64>(a, st); break;
     case 128: launch_fwd_f32_d<128>(a, st); break;
+    case 256: launch_fwd_f32_d<256>(a, st); break;
     default: break;
   }
 }

@@ -3,10 +3,10 @@
 // with fp32 inputs and IEEE fp32 dots (ta/interface.py:371, 389-391;
 // ta/kernels.py:258-270).  Same work decomposition as the 16-bit kernels:
 //   * forward (ta/kernels.py:185-284) and du/aX (ta/kernels.py:354-498): a
-//     workgroup of 4 waves x 16 rows owns up to 64 (token, head) rows of one
-//     sample (head-major: a wave's rows span at most two heads) and streams
-//     the sample's X rows once through a 3-deep ring of 16-key LDS tiles
-//     filled by buffer_load ... lds;
+//     workgroup of 4 waves x 16 rows owns the H heads of floor(64/H) tokens
+//     of one sample (head-major; with H not dividing 64 the last rows idle)
+//     and streams the sample's X rows once through a 3-deep ring of 16-key
+//     LDS tiles filled by buffer_load ... lds;
 //   * dX (ta/kernels.py:528-900): a workgroup owns up to 512 keys of one
 //     sample, 16 per wave per pass, and streams the sample's (token, head)
 //     rows of u and dAX through LDS in blocks of 32, summing over heads in
@@ -39,8 +39,9 @@ constexpr int kKT = 16;    // keys per LDS tile (forward, du)
 constexpr int kNBuf = 3;   // LDS ring depth
 constexpr int kRBlk = 32;  // (token, head) rows per LDS block (dX)
 
-// padded feature width: a multiple of 64 (the aX^T / du^T / dX^T tiling)
-inline int fp64_of(int F) { return (F + 63) / 64 * 64; }
+// padded feature width: a multiple of 64 (the aX^T / du^T / dX^T tiling) up
+// to 256; 512 above (the forward only)
+inline int fp64_of(int F) { return F > 256 ? 512 : (F + 63) / 64 * 64; }
 
 // LDS row stride (floats): 16 consecutive rows read at one column by the
 // S / dP products land on 16 distinct 16-byte bank groups
@@ -54,20 +55,25 @@ struct F32Smem {
 
 // LDS-DMA of rows [0, ROWS) of a row-major slab of F floats per row into a
 // [ROWS][XS] LDS block: NW waves move ROWS/NW rows each, one instruction per
-// row with lanes < FP/4 active (lanes whose 16-byte chunk lies past F, and
-// rows past the slab's `bytes`, read as zeros).
+// 64 16-byte chunks of a row (two at FP = 512) with chunks < FP/4 active
+// (chunks past F, and rows past the slab's `bytes`, read as zeros).
 template <int FP, int NW, int ROWS, int XS>
 __device__ __forceinline__ void dma_rows_f32(const float *src, int64_t bytes, int F, uint32_t base,
                                              int wave, int lane) {
+  constexpr int NI = (FP / 4 + 63) / 64;  // instructions per row
   const u32x4 rs = rsrc_words(src, bytes);
-  const uint32_t off = lane < F / 4 ? (uint32_t)lane * 16u : 0x80000000u;
-  if (lane < FP / 4) {
 #pragma unroll
-    for (int n = 0; n < ROWS / NW; ++n) {
-      const int r = wave * (ROWS / NW) + n;
-      int32_t voff;
-      asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(r * F * 4), "v"(off));
-      lds_dma16(rs, base + r * XS * 4, voff);
+  for (int part = 0; part < NI; ++part) {
+    const int ch = part * 64 + lane;
+    const uint32_t off = ch < F / 4 ? (uint32_t)ch * 16u : 0x80000000u;
+    if (ch < FP / 4) {
+#pragma unroll
+      for (int n = 0; n < ROWS / NW; ++n) {
+        const int r = wave * (ROWS / NW) + n;
+        int32_t voff;
+        asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(r * F * 4), "v"(off));
+        lds_dma16(rs, base + r * XS * 4 + part * 1024, voff);
+      }
     }
   }
 }
@@ -111,17 +117,20 @@ __global__ __launch_bounds__(256) void transpose_wv_f32_kernel(const float *__re
 }
 
 // Row geometry of a 64-row workgroup (forward and du): row = wave*16 + l16
-// is token row % TT of head row / TT, TT = 64 / H tokens.
+// is token row % TT of head row / TT, TT = floor(64 / H) tokens (rows past
+// H * TT idle).  A wave's rows span heads h_first..h_last.
 struct Rows64 {
-  int TT, tl, hh;
+  int TT, tl, hh, h_first, h_last;
   bool row_ok, wave_active;
   __device__ Rows64(int H, int ntok, int wave, int l16) {
     TT = kAbsorbRows / H;
     const int row = wave * 16 + l16;
     tl = row % TT;
     hh = row / TT;
-    row_ok = tl < ntok;
-    wave_active = (wave * 16) % TT < ntok;
+    row_ok = tl < ntok && hh < H;
+    wave_active = wave_any(row_ok);
+    h_first = wave * 16 / TT;
+    h_last = (wave * 16 + 15) / TT < H - 1 ? (wave * 16 + 15) / TT : H - 1;
   }
 };
 
@@ -130,15 +139,17 @@ struct Rows64 {
 // in the log2 domain against a lazily updated running max; split items
 // write projected fp32 partial rows + LSE for the combine.
 // ---------------------------------------------------------------------------
+// two workgroups per CU; one at FP = 512 (u operands and accumulators take
+// 256 registers)
 template <int FP>
-__global__ __launch_bounds__(256, 2) void absorb_fwd_f32_kernel(
+__global__ __launch_bounds__(256, FP > 256 ? 1 : 2) void absorb_fwd_f32_kernel(
     const float *__restrict__ u, const float *__restrict__ X, const float *__restrict__ wvt,
     float *__restrict__ O, float *__restrict__ lse, float *__restrict__ part_o,
     float *__restrict__ part_lse, const int32_t *__restrict__ items, int H, int F, int DH,
     float c) {
   using S = F32Smem<FP>;
   constexpr int Q = FP / 4, NA = FP / 64, XS = S::XS;
-  constexpr int kPerWave = kKT / 4;  // DMA instructions per wave per tile
+  constexpr int kPerWave = kKT / 4 * ((FP / 4 + 63) / 64);  // DMA instructions per wave per tile
   extern __shared__ __align__(16) float smem_f[];
 
   const PlanItem it = load_item(items, blockIdx.x);
@@ -265,10 +276,7 @@ __global__ __launch_bounds__(256, 2) void absorb_fwd_f32_kernel(
   // O^T (16 d x 16 rows) = W_V^T (16 d x f) (aX/l)^T: slice (a, r, b) takes
   // feature 64a + 16*lq + 4r + b in lane group lq -- the lane's own
   // accumulator acc[a][b][r] as B, wvt[h][d][64a + 16lq + 4r + b] as A
-  const int h_first = (wave * 16) / g.TT;
-  const int nh = g.TT >= 16 ? 1 : 16 / g.TT;
-  for (int hx = 0; hx < nh; ++hx) {
-    const int h = h_first + hx;
+  for (int h = g.h_first; h <= g.h_last; ++h) {
     for (int dt = 0; dt < DH / 16; ++dt) {
       const float *wrow = wvt + ((int64_t)h * DH + dt * 16 + l16) * FP + 16 * lq;
       f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -306,7 +314,7 @@ __global__ __launch_bounds__(256, 1) void absorb_du_f32_kernel(
     float scale) {
   using S = F32Smem<FP>;
   constexpr int Q = FP / 4, NA = FP / 64, XS = S::XS;
-  constexpr int kPerWave = kKT / 4;
+  constexpr int kPerWave = kKT / 4 * ((FP / 4 + 63) / 64);
   extern __shared__ __align__(16) float smem_f[];
 
   const PlanItem it = load_item(items, blockIdx.x);
@@ -566,9 +574,10 @@ void launch_bwd_fp(const AbsorbArgs &a, hipStream_t st) {
 
 }  // namespace
 
-// The fp32 matrix-core path takes H | 64 with H <= 8, D_KV a multiple of 4 up
-// to 256 (padded to a multiple of 64 inside the kernels) and D_H a multiple
-// of 16 up to 256.
+// The fp32 matrix-core path takes H <= 64 (floor(64/H) tokens per forward /
+// du workgroup), D_KV a multiple of 4 up to 256 (padded to a multiple of 64
+// inside the kernels; up to 512 in the forward, padded to 512) and D_H a
+// multiple of 16 up to 256.
 namespace {
 
 // dAX[t,h,f] = sum_d dO[t,h,d] W_V[f,h,d] in fp32 (ta/kernels.py:474-476, an
@@ -660,9 +669,13 @@ void launch_f32_absorb_dax(const AbsorbArgs &a, hipStream_t st) {
                      a.DH);
 }
 
+bool f32_absorb_fwd_supported(int H, int F, int DH) {
+  return H >= 1 && H <= kAbsorbRows && F >= 4 && F % 4 == 0 && F <= 512 && DH >= 16 &&
+         DH % 16 == 0 && DH <= 256;
+}
+
 bool f32_absorb_supported(int H, int F, int DH) {
-  return H >= 1 && H <= 8 && kAbsorbRows % H == 0 && F >= 4 && F % 4 == 0 && F <= 256 &&
-         DH >= 16 && DH % 16 == 0 && DH <= 256;
+  return f32_absorb_fwd_supported(H, F, DH) && F <= 256;
 }
 
 int64_t f32_absorb_wvt_elems(int H, int F, int DH) { return (int64_t)H * DH * fp64_of(F); }
@@ -679,6 +692,7 @@ void launch_f32_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
     case 128: launch_fwd_fp<128>(a, wvt, st); break;
     case 192: launch_fwd_fp<192>(a, wvt, st); break;
     case 256: launch_fwd_fp<256>(a, wvt, st); break;
+    case 512: launch_fwd_fp<512>(a, wvt, st); break;
     default: break;
   }
 }

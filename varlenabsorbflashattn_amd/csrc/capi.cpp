@@ -294,7 +294,7 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
       launch_simt_absorb_fwd<T>(a, st);
     }
   } else {
-    if (f32_absorb_supported(a.H, a.F, a.DH))
+    if (f32_absorb_fwd_supported(a.H, a.F, a.DH))
       launch_f32_absorb_fwd(a, st);
     else
       launch_simt_absorb_fwd<T>(a, st);

@@ -174,7 +174,8 @@ template <typename T> bool launch_mfma_absorb_dax(const AbsorbArgs &, hipStream_
 template <typename T> void launch_mfma_absorb_dx(const AbsorbArgs &, hipStream_t);
 
 // absorb_f32.hip: fp32 absorb on fp32 matrix cores (v_mfma_f32_16x16x4_f32)
-bool f32_absorb_supported(int H, int F, int DH);
+bool f32_absorb_supported(int H, int F, int DH);      // backward (D_KV <= 256)
+bool f32_absorb_fwd_supported(int H, int F, int DH);  // forward (D_KV <= 512)
 int64_t f32_absorb_wvt_elems(int H, int F, int DH);
 void launch_f32_absorb_fwd(const AbsorbArgs &, hipStream_t);
 // dAX = dO W_V^T in fp32 on fp32 matrix cores (F % 4 == 0, D_H % 16 == 0)

@@ -10,9 +10,9 @@
 // issues S^T = X U^T (X rows as the A operand) and aX^T += X^T P^T (X^T from
 // ds_read_b64_tr_b16) as 16x16x32 products, LDS operands read a few products
 // ahead, with the online softmax in the log2 domain.  The workgroup's rows
-// are head-major (a wave's 16 rows span at most two heads), so after the key
-// loop each wave rounds aX/l to the input dtype in registers and projects it
-// by its heads' W_V (16x16x32 products, W_V^T stored in the accumulators'
+// are head-major (a wave's 16 rows span few heads: two at H = 8), so after
+// the key loop each wave rounds aX/l to the input dtype in registers and
+// projects it by each of its heads' W_V (16x16x32 products, W_V^T stored in the accumulators'
 // f order): no LDS staging and no barrier in the epilogue.
 //
 // Folded projection (FOLD): instead of reading u (T_q x H x D_KV, written by
@@ -95,8 +95,8 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
   // Rows are head-major inside the workgroup: row r is token r % TT of head
-  // r / TT (TT = 64 / H tokens), so a wave's 16 rows span at most two heads
-  // and the W_V projection runs on the accumulators in registers.
+  // r / TT, so a wave's 16 rows span ceil(16 / TT) or one more heads and the
+  // W_V projection runs on the accumulators in registers, once per head.
   // TT = floor(64 / H) tokens per item: with H not dividing 64 the last
   // 64 - TT*H rows of the workgroup (head index >= H) stay idle.
   const int ntok = t1 - t0;
@@ -421,14 +421,14 @@ void launch_dh(const AbsorbArgs &a, const T *wvt, int FP, hipStream_t st) {
 
 using absorb::padded_f;
 
-// The matrix-core path takes H <= 16 (floor(64/H) >= 4 tokens per item, so
-// a wave's 16 rows span at most 4 heads), D_KV a multiple of 8 up to 256
-// (padded onto one of the compiled widths), and D_H in {16, 32, 64, 128,
-// 256}.
+// The matrix-core path takes H <= 64 (floor(64/H) >= 1 tokens per item; a
+// wave's 16 rows span up to 16 heads, each projected in the epilogue), D_KV
+// a multiple of 8 up to 256 (padded onto one of the compiled widths), and
+// D_H in {16, 32, 64, 128, 256}.
 template <typename T>
 bool mfma_absorb_supported(int H, int F, int DH) {
   const bool f_ok = F >= 8 && F % 8 == 0 && F <= kMaxF;
-  const bool h_ok = H >= 1 && H <= 16;
+  const bool h_ok = H >= 1 && H <= kAbsorbRows;
   const bool d_ok = DH == 16 || DH == 32 || DH == 64 || DH == 128 || DH == 256;
   return f_ok && h_ok && d_ok;
 }
@@ -463,6 +463,7 @@ int absorb_heads_per_wave(int H) {
 bool mfma_absorb_fold_supported(int H, int F, int DH) {
   if (!mfma_absorb_supported<bf16>(H, F, DH)) return false;  // F <= 256
   const int nhw = absorb_heads_per_wave(H);
+  if (nhw > 4) return false;  // FOLD variants form at most 4 heads per wave
   const int nhw_t = nhw == 1 ? 1 : nhw == 2 ? 2 : 4;
   if (nhw_t * (DH < 32 ? 1 : DH / 32) > 4) return false;
   return padded_f(F) <= 128 || (nhw_t <= 2 && DH <= 64);

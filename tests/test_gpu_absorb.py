@@ -99,8 +99,9 @@ HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 2
                (20, 16, 64),   # 3 tokens x 20 heads: up to 6 heads a wave (no fold)
                (40, 32, 64),   # 1 token x 40 heads, rows 40..63 idle
                (64, 16, 32),   # 1 token x 64 heads: 16 heads a wave
-               # 256 < D_KV <= 512: forward on the FP = 512 kernels (16-bit:
-               # 2-deep X ring), backward on the wave-per-row kernels
+               # 256 < D_KV <= 512: the FP = 512 kernels (16-bit: 2-deep
+               # forward ring, du and streamed dX in two f halves on paired
+               # workgroups); the fp32 backward on the wave-per-row kernels
                (8, 32, 384), (4, 64, 512), (2, 16, 264)]
 
 
@@ -111,8 +112,9 @@ def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
     """Matrix-core paths (bf16, fp16 and fp32) at head counts, head dims and
     feature widths off the benchmark shape, with the folded projection where
     its kernel takes the shape (at most 4 heads a wave).  d_kv = 50 takes the
-    wave-per-row path (not a multiple of 8 / 4).  D_KV in (256, 512] runs its
-    forward on matrix cores and its backward on the wave-per-row kernels."""
+    wave-per-row path (not a multiple of 8 / 4).  D_KV in (256, 512] runs on
+    matrix cores, except the fp32 backward (wave-per-row kernels).  The 70-token
+    sample has more than 64 (token, head) rows, so dX streams its row blocks."""
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)

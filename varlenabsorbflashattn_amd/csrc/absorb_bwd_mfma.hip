@@ -29,22 +29,42 @@ using namespace absorb;
 
 constexpr int kDuWaves = 4;  // 4 waves x 16 rows = one forward row tile
 
+// Above 256 features (FP = 512) the du / aX accumulators of all 32 f tiles
+// and the U^T / dAX^T operands would take 384 registers: there two
+// workgroups share a token tile, each forming S and dP over every feature
+// and accumulating du / aX for one half of the f tiles (NS = 2 slices).
+// Grid of NS = 2: blocks b and b + 8 of each 16 are the two halves of one
+// tile and run on one XCD, whose L2 serves the second stream of the tile's
+// X.  One workgroup per CU at FP = 512, two below.
+template <int FP>
+struct DuSlices {
+  static constexpr int NS = FP > kMaxF ? 2 : 1;
+};
+
 template <typename T, int FP>
-__global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
+__global__ __launch_bounds__(64 * kDuWaves, FP > kMaxF ? 1 : 2) void absorb_du_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ dax,
     const float *__restrict__ lse, const float *__restrict__ delta, T *__restrict__ du,
-    float *__restrict__ ax, const int32_t *__restrict__ items, int H, int F, float c,
-    float scale) {
+    float *__restrict__ ax, const int32_t *__restrict__ items, int n_items, int H, int F,
+    float c, float scale) {
   using M16 = Mfma16<T>;
   using v8 = typename Mfma<T>::v8;
   using S = AbsSmem<FP>;
-  constexpr int NK = FP / 32;   // 32-wide reduction chunks of S^T / dP^T
-  constexpr int NF = FP / 16;   // 16-row f tiles of aX^T / du^T
+  constexpr int NS = DuSlices<FP>::NS;
+  constexpr int NK = FP / 32;        // 32-wide reduction chunks of S^T / dP^T
+  constexpr int NF = FP / 16 / NS;   // 16-row f tiles of aX^T / du^T in this slice
   constexpr int kPerWave = kBK / kDuWaves;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T *smem = reinterpret_cast<T *>(smem_raw);
 
-  const PlanItem it = load_item(items, blockIdx.x);
+  int item = blockIdx.x, ft0 = 0;  // first f tile of this workgroup's slice
+  if constexpr (NS == 2) {
+    const int b = blockIdx.x;
+    item = (b / 16) * 8 + b % 8;
+    ft0 = ((b / 8) & 1) * NF;
+    if (item >= n_items) return;  // padding of the last group of 16
+  }
+  const PlanItem it = load_item(items, item);
   const int t0 = it.v[0], t1 = it.v[1], k0 = it.v[2], k1 = it.v[3];
   if (t1 <= t0) return;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -148,7 +168,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
       };
       v8 tring[kPre];
 #pragma unroll
-      for (int i = 0; i < kPre; ++i) tring[i] = top(i);
+      for (int i = 0; i < kPre; ++i) tring[i] = top(ft0 + i);
       const bool tail = kb + kBK > k1;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -174,7 +194,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
         const v8 a = tring[ft % kPre];
         aax[ft] = M16::mma(a, pb, aax[ft]);
         adu[ft] = M16::mma(a, sb, adu[ft]);
-        if (ft + kPre < NF) tring[ft % kPre] = top(ft + kPre);
+        if (ft + kPre < NF) tring[ft % kPre] = top(ft0 + ft + kPre);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -187,7 +207,7 @@ __global__ __launch_bounds__(64 * kDuWaves, 2) void absorb_du_kernel(
   const int64_t ro = ((int64_t)t0 * H + row) * F;
 #pragma unroll
   for (int ft = 0; ft < NF; ++ft) {
-    const int f = ft * 16 + lq * 4;  // element r is f + r of this lane's row
+    const int f = (ft0 + ft) * 16 + lq * 4;  // element r is f + r of this lane's row
     if (f >= F) continue;
     T4 wu;
 #pragma unroll
@@ -424,7 +444,7 @@ __device__ __forceinline__ void dx_halves(const D &d, typename D::T_ *dX, int kb
 // for both blocks first (X operands then dead, so the next sub-tile's X loads
 // right away), then accumulates dX^T in two f halves of 64 registers.
 template <typename T, int FP>
-__global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_res_kernel(
+__global__ __launch_bounds__(64 * kDxWaves, FP > kMaxF ? 1 : 2) void absorb_dx_res_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ dax,
     const float *__restrict__ lse, const float *__restrict__ delta, T *__restrict__ dX,
     const int32_t *__restrict__ items, int H, int F, float c, float scale) {
@@ -474,17 +494,29 @@ __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_res_kernel(
 
 // Items whose sample has more than 64 rows: per 128-key sub-tile the row
 // blocks stream through two buffers and dX^T accumulates over all of them.
+// At FP = 512 the accumulators of all 16 f tiles would take 256 registers:
+// two workgroups share an item (blocks b and b + 8 of each 16, on one XCD),
+// each forming S and dP over every feature and accumulating one half of the
+// f tiles (the du kernel's slicing).
 template <typename T, int FP>
-__global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_kernel(
+__global__ __launch_bounds__(64 * kDxWaves, FP > kMaxF ? 1 : 2) void absorb_dx_kernel(
     const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ dax,
     const float *__restrict__ lse, const float *__restrict__ delta, T *__restrict__ dX,
-    const int32_t *__restrict__ items, int H, int F, float c, float scale) {
+    const int32_t *__restrict__ items, int n_items, int H, int F, float c, float scale) {
   using D = DxItem<T, FP>;
   using v8 = typename D::M::v8;
-  constexpr int NF = D::NF;
+  constexpr int NS = DuSlices<FP>::NS;
+  constexpr int NF = D::NF / NS;  // 32-wide f tiles of this workgroup's slice
   constexpr int kPre = FP >= 224 ? 1 : 4;  // operand prefetch depth within the register budget
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const D d(u, X, dax, lse, delta, smem_raw, load_item(items, blockIdx.x), H, F);
+  int item = blockIdx.x, ft0 = 0;
+  if constexpr (NS == 2) {
+    const int b = blockIdx.x;
+    item = (b / 16) * 8 + b % 8;
+    ft0 = ((b / 8) & 1) * NF;
+    if (item >= n_items) return;  // padding of the last group of 16
+  }
+  const D d(u, X, dax, lse, delta, smem_raw, load_item(items, item), H, F);
   const int nblk = d.nblk();
   if (nblk * 32 <= kDxResidentRows) return;  // resident items: absorb_dx_res_kernel
   const int nsub = d.nsub();
@@ -515,7 +547,7 @@ __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_kernel(
       v8 pb[2], sb[2];
       d.template block_p_ds<kPre>(xf, buf, c, scale, pb, sb);
       v8 tring[kPre];
-      auto op = [&](int i) { return d.top(buf, (i / NF) & 1, (i / NF) >> 1, i % NF); };
+      auto op = [&](int i) { return d.top(buf, (i / NF) & 1, (i / NF) >> 1, ft0 + i % NF); };
 #pragma unroll
       for (int i = 0; i < kPre; ++i) tring[i] = op(i);
       __builtin_amdgcn_sched_barrier(0);
@@ -528,7 +560,7 @@ __global__ __launch_bounds__(64 * kDxWaves, 2) void absorb_dx_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (wave_active && key < d.k1) d.store(dX, key, 0, acc);
+    if (wave_active && key < d.k1) d.store(dX, key, ft0, acc);
   }
   wait_vmcnt<0>();
 }
@@ -612,11 +644,13 @@ __global__ __launch_bounds__(64) void absorb_dax_kernel(const T *__restrict__ dO
 
 template <typename T, int FP>
 void launch_du_fp(const AbsorbArgs &a, hipStream_t st) {
-  const int smem = AbsSmem<FP>::kLoopBytes;
+  const int smem = kNBuf * AbsSmem<FP>::kTile * 2;  // the du ring is 3 deep at every FP
   allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_du_kernel<T, FP>), smem);
-  hipLaunchKernelGGL((absorb_du_kernel<T, FP>), dim3((unsigned)a.n_qseg), dim3(64 * kDuWaves), smem,
+  const int64_t grid = DuSlices<FP>::NS == 2 ? (a.n_qseg + 7) / 8 * 16 : a.n_qseg;
+  hipLaunchKernelGGL((absorb_du_kernel<T, FP>), dim3((unsigned)grid), dim3(64 * kDuWaves), smem,
                      st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in, a.delta,
-                     (T *)a.du, a.ax, a.qseg_items, a.H, a.F, a.scale * kLog2e, a.scale);
+                     (T *)a.du, a.ax, a.qseg_items, (int)a.n_qseg, a.H, a.F, a.scale * kLog2e,
+                     a.scale);
 }
 
 template <typename T, int FP>
@@ -634,9 +668,10 @@ void launch_dx_fp(const AbsorbArgs &a, hipStream_t st) {
   }
   if (n_str > 0) {
     allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_dx_kernel<T, FP>), smem);
-    hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)n_str), dim3(64 * kDxWaves),
+    const int64_t grid = DuSlices<FP>::NS == 2 ? (n_str + 7) / 8 * 16 : n_str;
+    hipLaunchKernelGGL((absorb_dx_kernel<T, FP>), dim3((unsigned)grid), dim3(64 * kDxWaves),
                        smem, st, (const T *)a.u, (const T *)a.X, (const T *)a.dax, a.lse_in,
-                       a.delta, (T *)a.dX, a.kv_items + n_res * 8, a.H, a.F,
+                       a.delta, (T *)a.dX, a.kv_items + n_res * 8, (int)n_str, a.H, a.F,
                        a.scale * kLog2e, a.scale);
   }
 }
@@ -652,6 +687,7 @@ void launch_mfma_absorb_du(const AbsorbArgs &a, hipStream_t st) {
     case 192: launch_du_fp<T, 192>(a, st); break;
     case 224: launch_du_fp<T, 224>(a, st); break;
     case 256: launch_du_fp<T, 256>(a, st); break;
+    case 512: launch_du_fp<T, 512>(a, st); break;
     default: break;
   }
 }
@@ -665,6 +701,7 @@ void launch_mfma_absorb_dx(const AbsorbArgs &a, hipStream_t st) {
     case 192: launch_dx_fp<T, 192>(a, st); break;
     case 224: launch_dx_fp<T, 224>(a, st); break;
     case 256: launch_dx_fp<T, 256>(a, st); break;
+    case 512: launch_dx_fp<T, 512>(a, st); break;
     default: break;
   }
 }

@@ -433,8 +433,8 @@ bool mfma_absorb_supported(int H, int F, int DH) {
   return f_ok && h_ok && d_ok;
 }
 
-// The forward kernel also takes 256 < D_KV <= 512 (FP = 512, 2-deep ring);
-// the backward kernels of those widths are the wave-per-row ones.
+// The forward and backward kernels also take 256 < D_KV <= 512 (FP = 512:
+// a 2-deep forward ring, one workgroup per CU in du and dX).
 template <typename T>
 bool mfma_absorb_fwd_supported(int H, int F, int DH) {
   if (F > kMaxF && F <= kMaxFwdF && F % 8 == 0) return mfma_absorb_supported<T>(H, 8, DH);

@@ -9,8 +9,9 @@ namespace absorb {
 
 constexpr int kBK = 32;     // keys per LDS tile
 constexpr int kNBuf = 3;    // LDS ring depth
-constexpr int kMaxF = 256;  // D_KV handled by these kernels (padded to 32)
-constexpr int kMaxFwdF = 512;  // D_KV of the forward kernel (2-deep ring above kMaxF)
+constexpr int kMaxF = 256;  // D_KV of the compiled widths up to 256 (padded to 32)
+constexpr int kMaxFwdF = 512;  // above kMaxF: FP = 512 (2-deep forward ring, one du / dX
+                               // workgroup per CU)
 
 // Row padding of the staged tiles (elements), by operand read pattern,
 // measured on gfx950 at 12 waves per CU with FP = 256: the 16x16x32 kernels
@@ -74,7 +75,7 @@ __device__ __forceinline__ void dma_block(const void *src, uint32_t bytes, int F
 }
 
 // F padded up to the next width the matrix-core kernels are compiled for
-// (64, 128, 192, 224, 256; 512 for the forward): the padding reads as zeros
+// (64, 128, 192, 224, 256, 512): the padding reads as zeros
 // and every store is bounded by F itself, so any F % 8 == 0 up to the
 // largest width runs on one of them.
 inline int padded_f(int F) {
@@ -83,7 +84,7 @@ inline int padded_f(int F) {
   if (f32 <= 128) return 128;
   if (f32 <= 192) return 192;
   if (f32 <= 224) return 224;
-  return f32 <= 256 ? 256 : 512;  // 512: the forward kernel only
+  return f32 <= 256 ? 256 : 512;
 }
 
 }  // namespace absorb

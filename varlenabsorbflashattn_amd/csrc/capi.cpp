@@ -306,7 +306,7 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
 template <typename T>
 void absorb_bwd_all(const AbsorbArgs &a, hipStream_t st) {
   bool mfma = false;
-  if constexpr (sizeof(T) == 2) mfma = mfma_absorb_supported<T>(a.H, a.F, a.DH);
+  if constexpr (sizeof(T) == 2) mfma = mfma_absorb_fwd_supported<T>(a.H, a.F, a.DH);
   // the matrix-core dAX kernel also writes delta (sum_d dO O) for its rows
   bool dax_done = false;
   if constexpr (sizeof(T) == 2) dax_done = launch_mfma_absorb_dax<T>(a, st);

@@ -213,7 +213,11 @@ VAFA_API int vafa_varlen_bwd_stage(int32_t stage, const void *q, const void *k, 
                                    float scale, void *workspace, int64_t workspace_bytes,
                                    void *stream);
 
-/* Workspace bytes needed by vafa_absorb_fwd / vafa_absorb_bwd. */
+/* Workspace bytes needed by vafa_absorb_fwd / vafa_absorb_bwd.  With
+ * D_KV % 8 != 0 they include copies of u, X and W_V (and of the gradients)
+ * whose D_KV is zero-padded to a multiple of 8, sized for fp32: calls whose
+ * D_KV is not a whole number of 16-byte chunks run on the matrix-core
+ * kernels over them. */
 VAFA_API int64_t vafa_absorb_fwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);
 VAFA_API int64_t vafa_absorb_bwd_workspace(const vafa_plan_info *info, int64_t D_KV, int64_t D_H);
 

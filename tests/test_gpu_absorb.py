@@ -88,7 +88,9 @@ def test_absorb_bf16_parity(device, name, q_lens, k_lens):
 # head counts and head dims off the benchmark shape (rows of a workgroup are
 # laid out head-major, floor(64 / H) tokens per head)
 HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 216),
-               (2, 16, 50),    # d_kv not a multiple of 8: the wave-per-row path
+               # d_kv not a whole number of 16-byte chunks: zero-padded copies
+               # (to 56, 104, 512) on the matrix cores
+               (2, 16, 50), (8, 32, 100), (3, 16, 509),
                (6, 32, 96),    # H not dividing 64 (10 tokens x 6 heads, 3 heads a wave)
                (16, 32, 128),  # 4 tokens x 16 heads: 4 heads a wave
                (12, 16, 64),   # 5 tokens x 12 heads
@@ -111,10 +113,11 @@ HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 2
 def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
     """Matrix-core paths (bf16, fp16 and fp32) at head counts, head dims and
     feature widths off the benchmark shape, with the folded projection where
-    its kernel takes the shape (at most 4 heads a wave).  d_kv = 50 takes the
-    wave-per-row path (not a multiple of 8 / 4).  D_KV in (256, 512] runs on
-    matrix cores, except the fp32 backward (wave-per-row kernels).  The 70-token
-    sample has more than 64 (token, head) rows, so dX streams its row blocks."""
+    its kernel takes the shape (at most 4 heads a wave).  d_kv = 50, 100 (16-bit)
+    and 509 run on copies zero-padded to a multiple of 8.  D_KV in (256, 512]
+    runs on matrix cores, except the fp32 backward (wave-per-row kernels).  The
+    70-token sample has more than 64 (token, head) rows, so dX streams its row
+    blocks."""
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)

@@ -252,17 +252,53 @@ struct AbsorbWs {
   float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *dax = nullptr, *ax = nullptr,
         *dwv_part = nullptr;
   void *wvt = nullptr, *wkt = nullptr;
+  // D_KV padded to a multiple of 8: copies of u, X, W_V and (backward) the
+  // padded du, dX, dW_V
+  void *pu = nullptr, *pX = nullptr, *pW = nullptr, *pdu = nullptr, *pdX = nullptr,
+       *pdW = nullptr;
   int64_t n_tchunks = 0, tchunk = 0;
   int64_t bytes = 0;
 };
 
 constexpr int64_t kDwvChunks = 64;
 
-AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F, int64_t DH, bool bwd,
+// D_KV that is not a whole number of 16-byte chunks (8 16-bit or 4 fp32
+// elements) runs on the matrix-core kernels over copies of u, X and W_V
+// whose D_KV is zero-padded to a multiple of 8, when they take the padded
+// shape: the zero features add exact zeros to every product and leave zero
+// columns in du, dX and dW_V, which are not copied back.
+inline int64_t absorb_fpad(int64_t F) { return (F + 7) / 8 * 8; }
+
+bool absorb_pad(int64_t H, int64_t F, int64_t DH, int32_t dtype, bool bwd) {
+  if (F % (dtype == VAFA_F32 ? 4 : 8) == 0) return false;
+  const int h = (int)H, fp = (int)absorb_fpad(F), dh = (int)DH;
+  switch (dtype) {
+    case VAFA_F32: return bwd ? f32_absorb_supported(h, fp, dh) : f32_absorb_fwd_supported(h, fp, dh);
+    case VAFA_BF16: return mfma_absorb_fwd_supported<bf16>(h, fp, dh);
+    case VAFA_F16: return mfma_absorb_fwd_supported<f16>(h, fp, dh);
+    default: return false;
+  }
+}
+
+// The workspace functions do not see the dtype: with D_KV % 8 != 0 they
+// include the padded copies (sized for fp32) and size the internal buffers
+// for the padded width.
+AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F0, int64_t DH, bool bwd,
                       bool fold = false) {
   Carver c(ws);
   AbsorbWs w;
   const int64_t H = info->H, Tq = info->T_q;
+  const int64_t F = absorb_fpad(F0);  // >= F0; == F0 when F0 % 8 == 0
+  if (F0 % 8 != 0) {
+    w.pu = c.take<void>(Tq * H * F * 4);
+    w.pX = c.take<void>(info->T_k * F * 4);
+    w.pW = c.take<void>(F * H * DH * 4);
+    if (bwd) {
+      w.pdu = c.take<void>(Tq * H * F * 4);
+      w.pdX = c.take<void>(info->T_k * F * 4);
+      w.pdW = c.take<void>(F * H * DH * 4);
+    }
+  }
   if (!bwd) {
     w.part_o = c.take<float>(info->n_part_rows * H * DH * 4);
     w.part_lse = c.take<float>(info->n_part_rows * H * 4);
@@ -688,17 +724,27 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
     return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
                 (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
   AbsorbArgs a{};
   a.u = u; a.X = X; a.wv = W_V; a.O = O; a.lse = lse;
   a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt;
+  int64_t F = D_KV;
+  if (absorb_pad(info->H, D_KV, D_H, dtype, false)) {
+    F = absorb_fpad(D_KV);
+    const int eb = elem_bytes(dtype);
+    launch_pad_cols(u, w.pu, info->T_q * info->H, D_KV, F, eb, st);
+    launch_pad_cols(X, w.pX, info->T_k, D_KV, F, eb, st);
+    launch_pad_cols(W_V, w.pW, 1, D_KV * info->H * D_H, F * info->H * D_H, eb, st);
+    a.u = w.pu; a.X = w.pX; a.wv = w.pW;
+  }
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
   a.comb_items = plan_dev + info->off_comb; a.n_comb = info->n_comb;
   a.comb_rows = (int)info->max_comb_rows;
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv; a.n_kv_res = info->n_kv_res;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;
-  a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
-  if (int rc = by_dtype<AFwd>(dtype, a, (hipStream_t)stream)) return rc;
+  a.H = (int)info->H; a.F = (int)F; a.DH = (int)D_H; a.scale = scale;
+  if (int rc = by_dtype<AFwd>(dtype, a, st)) return rc;
   return check_launch("vafa_absorb_fwd");
 }
 
@@ -836,9 +882,20 @@ int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O
   if (workspace_bytes < w.bytes || (w.bytes > 0 && workspace == nullptr))
     return fail(VAFA_ERR_WORKSPACE, "workspace of %lld bytes, %lld needed",
                 (long long)workspace_bytes, (long long)w.bytes);
+  const hipStream_t st = (hipStream_t)stream;
   AbsorbArgs a{};
   a.u = u; a.X = X; a.wv = W_V; a.O_in = O; a.dO = dO; a.lse_in = lse;
   a.du = du; a.dX = dX; a.dwv = dW_V;
+  const bool pad = absorb_pad(info->H, D_KV, D_H, dtype, true);
+  const int64_t F = pad ? absorb_fpad(D_KV) : D_KV;
+  const int eb = elem_bytes(dtype);
+  if (pad) {
+    launch_pad_cols(u, w.pu, info->T_q * info->H, D_KV, F, eb, st);
+    launch_pad_cols(X, w.pX, info->T_k, D_KV, F, eb, st);
+    launch_pad_cols(W_V, w.pW, 1, D_KV * info->H * D_H, F * info->H * D_H, eb, st);
+    a.u = w.pu; a.X = w.pX; a.wv = w.pW;
+    a.du = w.pdu; a.dX = w.pdX; a.dwv = w.pdW;
+  }
   a.delta = w.delta; a.dax = w.dax; a.ax = w.ax; a.dwv_part = w.dwv_part;
   a.n_tchunks = w.n_tchunks; a.tchunk = w.tchunk;
   a.items = plan_dev + info->off_fwd; a.n_items = info->n_fwd;
@@ -847,8 +904,13 @@ int vafa_absorb_bwd(const void *u, const void *X, const void *W_V, const void *O
   a.kv_items = plan_dev + info->off_kv; a.n_kv = info->n_kv; a.n_kv_res = info->n_kv_res;
   a.qseg_items = plan_dev + info->off_qt; a.n_qseg = info->n_qt;
   a.T_q = info->T_q; a.T_k = info->T_k;
-  a.H = (int)info->H; a.F = (int)D_KV; a.DH = (int)D_H; a.scale = scale;
-  if (int rc = by_dtype<ABwd>(dtype, a, (hipStream_t)stream)) return rc;
+  a.H = (int)info->H; a.F = (int)F; a.DH = (int)D_H; a.scale = scale;
+  if (int rc = by_dtype<ABwd>(dtype, a, st)) return rc;
+  if (pad) {
+    launch_unpad_cols(w.pdu, du, info->T_q * info->H, D_KV, F, eb, st);
+    launch_unpad_cols(w.pdX, dX, info->T_k, D_KV, F, eb, st);
+    launch_unpad_cols(w.pdW, dW_V, 1, D_KV * info->H * D_H, F * info->H * D_H, eb, st);
+  }
   return check_launch("vafa_absorb_bwd");
 }
 

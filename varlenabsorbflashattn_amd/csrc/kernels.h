@@ -115,6 +115,12 @@ void launch_wgrad(const void *a, const void *b, float *part, void *out, int64_t 
 // (elem_bytes: 2 for 16-bit elements, 4 for fp32)
 void launch_pad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t);
 void launch_unpad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t);
+// rows [rows, n] -> zero-padded [rows, m] (m >= n), and the first n columns
+// back (elem_bytes 2 or 4)
+void launch_pad_cols(const void *src, void *dst, int64_t rows, int64_t n, int64_t m,
+                     int elem_bytes, hipStream_t);
+void launch_unpad_cols(const void *src, void *dst, int64_t rows, int64_t n, int64_t m,
+                       int elem_bytes, hipStream_t);
 // out[o] = sum_c part[c * n_out + o] in chunk order, rounded to T
 template <typename T>
 void launch_chunk_sum(const float *part, void *out, int64_t n_out, int64_t n_chunks, hipStream_t);

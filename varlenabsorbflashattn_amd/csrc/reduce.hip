@@ -458,6 +458,29 @@ __global__ __launch_bounds__(256) void unpad16_kernel(const u32x4 *__restrict__ 
   dst[r * cpr + c] = src[r * 2 * cpr + c];
 }
 
+// [rows, n] -> [rows, m] (m >= n) with zero columns n..m-1, and back
+// (element type E of the operand's width: absorb D_KV padded to a whole
+// number of 16-byte chunks)
+template <typename E>
+__global__ __launch_bounds__(256) void pad_cols_kernel(const E *__restrict__ src,
+                                                       E *__restrict__ dst, int64_t rows,
+                                                       int64_t n, int64_t m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * m) return;
+  const int64_t r = i / m, c = i % m;
+  dst[i] = c < n ? src[r * n + c] : E(0);
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void unpad_cols_kernel(const E *__restrict__ src,
+                                                         E *__restrict__ dst, int64_t rows,
+                                                         int64_t n, int64_t m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * n) return;
+  const int64_t r = i / n, c = i % n;
+  dst[i] = src[r * m + c];
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -561,6 +584,28 @@ void launch_pad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipS
   const int cpr = elem_bytes;  // 16 elements = elem_bytes 16-byte chunks
   hipLaunchKernelGGL(pad16_kernel, dim3(blocks_for(rows * 2 * cpr)), dim3(256), 0, st,
                      (const u32x4 *)src, (u32x4 *)dst, rows, cpr);
+}
+
+void launch_pad_cols(const void *src, void *dst, int64_t rows, int64_t n, int64_t m,
+                     int elem_bytes, hipStream_t st) {
+  if (rows <= 0 || m <= 0) return;
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(pad_cols_kernel<uint32_t>, dim3(blocks_for(rows * m)), dim3(256), 0, st,
+                       (const uint32_t *)src, (uint32_t *)dst, rows, n, m);
+  else
+    hipLaunchKernelGGL(pad_cols_kernel<uint16_t>, dim3(blocks_for(rows * m)), dim3(256), 0, st,
+                       (const uint16_t *)src, (uint16_t *)dst, rows, n, m);
+}
+
+void launch_unpad_cols(const void *src, void *dst, int64_t rows, int64_t n, int64_t m,
+                       int elem_bytes, hipStream_t st) {
+  if (rows <= 0 || n <= 0) return;
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(unpad_cols_kernel<uint32_t>, dim3(blocks_for(rows * n)), dim3(256), 0,
+                       st, (const uint32_t *)src, (uint32_t *)dst, rows, n, m);
+  else
+    hipLaunchKernelGGL(unpad_cols_kernel<uint16_t>, dim3(blocks_for(rows * n)), dim3(256), 0,
+                       st, (const uint16_t *)src, (uint16_t *)dst, rows, n, m);
 }
 
 void launch_unpad16(const void *src, void *dst, int64_t rows, int elem_bytes, hipStream_t st) {

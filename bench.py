@@ -381,8 +381,7 @@ def bench_absorb_shapes(iters):
     shapes (ta/interface.py:176, 200-201), each on its matrix-core path:
     H = 16 and H = 6 (not dividing 64), D_H = 256, and D_KV = 512 (the FP = 512
     kernels), in bf16; and H = 16 and D_KV = 512 in fp32 (the fp32 matrix-core
-    kernels; the fp32 D_KV = 512 backward runs on the wave-per-row kernels and
-    is not timed; GB/s counts 4-byte elements there).
+    kernels; GB/s counts 4-byte elements there).
     Returns {name: line}."""
     import torch
     from varlenabsorbflashattn_amd import workloads as W
@@ -391,7 +390,7 @@ def bench_absorb_shapes(iters):
     bf, f32 = torch.bfloat16, torch.float32
     for H, DH, F, bwd, dt in ((16, 16, 256, True, bf), (6, 32, 96, True, bf),
                               (8, 256, 256, True, bf), (8, 32, 512, True, bf),
-                              (16, 16, 256, True, f32), (8, 32, 512, False, f32)):
+                              (16, 16, 256, True, f32), (8, 32, 512, True, f32)):
         tag = "_fp32" if dt == f32 else ""
         case = W.AbsorbCase(f"c4_lengths_H{H}_DH{DH}_F{F}{tag}", c4.q_lens, c4.k_lens, H, DH,
                             F, dt)

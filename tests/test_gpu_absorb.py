@@ -103,7 +103,7 @@ HEAD_SHAPES = [(1, 32, 64), (2, 64, 128), (4, 16, 256), (4, 128, 192), (8, 64, 2
                (64, 16, 32),   # 1 token x 64 heads: 16 heads a wave
                # 256 < D_KV <= 512: the FP = 512 kernels (16-bit: 2-deep
                # forward ring, du and streamed dX in two f halves on paired
-               # workgroups); the fp32 backward on the wave-per-row kernels
+               # workgroups; fp32: du in two halves, dX at one workgroup per CU)
                (8, 32, 384), (4, 64, 512), (2, 16, 264)]
 
 
@@ -115,9 +115,8 @@ def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
     feature widths off the benchmark shape, with the folded projection where
     its kernel takes the shape (at most 4 heads a wave).  d_kv = 50, 100 (16-bit)
     and 509 run on copies zero-padded to a multiple of 8.  D_KV in (256, 512]
-    runs on matrix cores, except the fp32 backward (wave-per-row kernels).  The
-    70-token sample has more than 64 (token, head) rows, so dX streams its row
-    blocks."""
+    runs on matrix cores in both directions.  The 70-token sample has more than
+    64 (token, head) rows, so dX streams its row blocks."""
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)

@@ -310,14 +310,25 @@ template <int FP>
 __global__ __launch_bounds__(256, 1) void absorb_du_f32_kernel(
     const float *__restrict__ u, const float *__restrict__ X, const float *__restrict__ lse,
     const float *__restrict__ delta, const float *__restrict__ dax, float *__restrict__ du,
-    float *__restrict__ ax_ws, const int32_t *__restrict__ items, int H, int F, float c,
-    float scale) {
+    float *__restrict__ ax_ws, const int32_t *__restrict__ items, int n_items, int H, int F,
+    float c, float scale) {
   using S = F32Smem<FP>;
-  constexpr int Q = FP / 4, NA = FP / 64, XS = S::XS;
+  // FP = 512: two workgroups of one XCD share a token tile (blocks b and
+  // b + 8 of each 16), each forming S and dP over every feature and
+  // accumulating du / aX for one half of the 64-feature groups
+  constexpr int NS = FP > 256 ? 2 : 1;
+  constexpr int Q = FP / 4, NA = FP / 64 / NS, XS = S::XS;
   constexpr int kPerWave = kKT / 4 * ((FP / 4 + 63) / 64);
   extern __shared__ __align__(16) float smem_f[];
 
-  const PlanItem it = load_item(items, blockIdx.x);
+  int item = blockIdx.x, a0 = 0;  // first 64-feature group of this slice
+  if constexpr (NS == 2) {
+    const int b = blockIdx.x;
+    item = (b / 16) * 8 + b % 8;
+    a0 = ((b / 8) & 1) * NA;
+    if (item >= n_items) return;  // padding of the last group of 16
+  }
+  const PlanItem it = load_item(items, item);
   const int t0 = it.v[0], t1 = it.v[1], k0 = it.v[2], k1 = it.v[3];
   if (t1 <= t0) return;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -386,7 +397,7 @@ __global__ __launch_bounds__(256, 1) void absorb_du_f32_kernel(
         const float *xt = xs + (4 * lq + j4) * XS + 4 * l16;
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
-          const f32x4 xv = *reinterpret_cast<const f32x4 *>(xt + 64 * a);
+          const f32x4 xv = *reinterpret_cast<const f32x4 *>(xt + 64 * (a0 + a));
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
             adu[a][b] = mma4(xv[b], ds[j4], adu[a][b]);
@@ -404,7 +415,7 @@ __global__ __launch_bounds__(256, 1) void absorb_du_f32_kernel(
   for (int a = 0; a < NA; ++a)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int f = 64 * a + 16 * lq + 4 * r;
+      const int f = 64 * (a0 + a) + 16 * lq + 4 * r;
       if (f >= F) continue;
       f32x4 wu, wa;
 #pragma unroll
@@ -426,8 +437,10 @@ __global__ __launch_bounds__(256, 1) void absorb_du_f32_kernel(
 // every wave 16 keys (their X rows are the B operand, in registers); the rows
 // stream through LDS in blocks of 32 with their LSE and delta.
 // ---------------------------------------------------------------------------
+// two workgroups per CU; one at FP = 512 (X operands and dX accumulators
+// take 256 registers)
 template <int FP>
-__global__ __launch_bounds__(256, 2) void absorb_dx_f32_kernel(
+__global__ __launch_bounds__(256, FP > 256 ? 1 : 2) void absorb_dx_f32_kernel(
     const float *__restrict__ u, const float *__restrict__ X, const float *__restrict__ lse,
     const float *__restrict__ delta, const float *__restrict__ dax, float *__restrict__ dX,
     const int32_t *__restrict__ items, int H, int F, float c, float scale) {
@@ -557,10 +570,11 @@ void launch_bwd_fp(const AbsorbArgs &a, hipStream_t st) {
   if (a.n_qseg > 0) {
     const int smem = F32Smem<FP>::kFwdBytes;
     allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_du_f32_kernel<FP>), smem);
-    hipLaunchKernelGGL(absorb_du_f32_kernel<FP>, dim3((unsigned)a.n_qseg), dim3(256), smem, st,
+    const int64_t grid = FP > 256 ? (a.n_qseg + 7) / 8 * 16 : a.n_qseg;
+    hipLaunchKernelGGL(absorb_du_f32_kernel<FP>, dim3((unsigned)grid), dim3(256), smem, st,
                        (const float *)a.u, (const float *)a.X, a.lse_in, a.delta,
-                       (const float *)a.dax, (float *)a.du, a.ax, a.qseg_items, a.H, a.F,
-                       a.scale * kLog2e, a.scale);
+                       (const float *)a.dax, (float *)a.du, a.ax, a.qseg_items, (int)a.n_qseg,
+                       a.H, a.F, a.scale * kLog2e, a.scale);
   }
   if (a.n_kv > 0) {
     const int smem = F32Smem<FP>::kDxBytes;
@@ -674,9 +688,7 @@ bool f32_absorb_fwd_supported(int H, int F, int DH) {
          DH % 16 == 0 && DH <= 256;
 }
 
-bool f32_absorb_supported(int H, int F, int DH) {
-  return f32_absorb_fwd_supported(H, F, DH) && F <= 256;
-}
+bool f32_absorb_supported(int H, int F, int DH) { return f32_absorb_fwd_supported(H, F, DH); }
 
 int64_t f32_absorb_wvt_elems(int H, int F, int DH) { return (int64_t)H * DH * fp64_of(F); }
 
@@ -703,6 +715,7 @@ void launch_f32_absorb_du_dx(const AbsorbArgs &a, hipStream_t st) {
     case 128: launch_bwd_fp<128>(a, st); break;
     case 192: launch_bwd_fp<192>(a, st); break;
     case 256: launch_bwd_fp<256>(a, st); break;
+    case 512: launch_bwd_fp<512>(a, st); break;
     default: break;
   }
 }

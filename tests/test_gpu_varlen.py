@@ -124,10 +124,10 @@ F32_CASES = [
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("name,q_lens,k_lens", F32_CASES, ids=[c[0] for c in F32_CASES])
 def test_varlen_fp32_matrix_cores(device, name, q_lens, k_lens, D):
-    """fp32 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32): forward at D in
-    {32, 64, 128, 256}, gradients at D in {32, 64, 128} (D=256 gradients on the
-    wave-per-row kernels), D=16 over zero-padded D=32 copies; against the fp64
-    oracle at the fp32 bound (1e-4 / 1e-5), including split-K partials,
+    """fp32 on the fp32 matrix cores: forward at D in {32, 64, 128, 256} and
+    gradients at D in {32, 64, 128} on v_mfma_f32_32x32x2_f32, D=256 gradients
+    on v_mfma_f32_16x16x4_f32, D=16 over zero-padded D=32 copies; against the
+    fp64 oracle at the fp32 bound (1e-4 / 1e-5), including split-K partials,
     256-row tiles (walked as two 128-row halves in dQ at D=128), empty
     segments and key tails."""
     print(f"[varlen f32 mfma] {name} q={q_lens} k={k_lens} D={D}", flush=True)

@@ -150,14 +150,13 @@ void varlen_fwd_all(const VarlenArgs &a, hipStream_t st) {
                         a.comb_rows, st);
 }
 
-// Backward stages.  16-bit matrix-core kernels for D in {32, 64, 128, 256},
-// fp32 ones for D in {32, 64, 128}; D=16 (below the 32-wide output tiles)
-// reaches them padded to 32 from vafa_varlen_bwd, and fp32 D=256 and the
-// stage entry points' D=16 take the wave-per-row kernels.  Segments the plan
-// fuses (few queries, D <= 64) run
+// Backward stages.  Matrix-core kernels for D in {32, 64, 128, 256} (16-bit
+// and fp32); D=16 (below the 32-wide output tiles) reaches them padded to 32
+// from vafa_varlen_bwd, and the stage entry points' D=16 takes the
+// wave-per-row kernels.  Segments the plan fuses (few queries, D <= 64) run
 // dQ/dK/dV in the fused key-major kernel, whose dQ partials are summed in
-// order; without matrix cores their key tiles go to the plain dK/dV kernel
-// and their dQ to the dQ pass over every forward item.
+// order; without it (fp32) their key tiles go to the plain dK/dV kernel and
+// their dQ to the dQ pass over every forward item.
 inline bool mfma_bwd_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
 template <typename T>
@@ -210,7 +209,8 @@ void varlen_bwd_stage(int stage, const VarlenArgs &a, hipStream_t st) {
                               st);
       }
     }
-    // fp32: the fp32 matrix-core kernels at D in {32, 64}, else wave-per-key
+    // fp32: the fp32 matrix-core kernels (D=16 only from the stage API, on
+    // the wave-per-key kernel)
     const bool f32m = sizeof(T) == 4 && f32_varlen_bwd_mfma_d(a.D);
     if (!mfma) {
       if (f32m)

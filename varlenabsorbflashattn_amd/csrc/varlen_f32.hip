@@ -245,9 +245,10 @@ void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward (D in {32, 64, 128}).  At D = 128 the operands held in registers
-// and the accumulators take more than half the register file, so those
-// workgroups run one wave per SIMD; at D = 256 they would not fit at all.
+// Backward (D in {32, 64, 128}; D = 256 below, on 16x16x4 products).  At
+// D = 128 the operands held in registers and the accumulators take more than
+// half the register file, so those workgroups run one wave per SIMD; at
+// D = 256 they would not fit at all.
 //
 // dQ, query-major over the forward's items (split items write scaled fp32
 // partial rows that the ordered sum adds): per 32-key tile
@@ -619,6 +620,335 @@ __global__ __launch_bounds__(64 * NW, NW == 8 || D >= 128 ? 1 : 2) void varlen_d
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward at D = 256 on v_mfma_f32_16x16x4_f32.  The 32x32x2 kernels above
+// hold a row's (or key's) whole Q^T / dO^T (or K^T / V^T) operands, 2 * D/2
+// floats, beside D/32 accumulator tiles: 512 registers and more at D = 256.
+// With 16 rows (keys) per wave each lane group lq holds only the quarter of
+// the features it reduces over (Q = D/4 per operand), as the fp32 absorb
+// kernels do:
+//   * products over d (S, dP): step i takes feature Q*lq + i in lane group
+//     lq, so a lane reads Q consecutive floats of its LDS row;
+//   * products over keys / rows (dQ^T, dV^T, dK^T): output tile (a, b) holds
+//     feature 64a + 4m + b in its row m and step j4 takes the key / row
+//     4*lq + j4 -- the one whose S / dS element j4 the lane holds -- so the A
+//     operand is one 16-byte LDS read over b and the B operand needs no
+//     exchange; a lane's accumulators hold features 64a + 16*lq + 4r + b,
+//     stored as 16-byte runs.
+// 16-row K / V (dQ) or Q / dO (dK/dV) tiles, double-buffered, staged by
+// buffer_load ... lds, one instruction per row (D = 256 floats = 64 lanes x
+// 16 bytes).
+// ---------------------------------------------------------------------------
+constexpr int kX4Rows = 16;  // rows per LDS tile
+
+template <int D>
+struct F32x4Smem {
+  static constexpr int XS = D + 4;                  // row stride (floats)
+  static constexpr int kTile = kX4Rows * XS;        // one tile
+  static constexpr int kBuf = 2 * kTile + 2 * kX4Rows;  // two tiles (+ LSE, delta)
+  static constexpr int kBytes = 2 * kBuf * 4;       // double buffered
+};
+
+// LDS-DMA of token rows [0, 16) of one head of a [T, H, D] fp32 tensor (row
+// r at byte r*row_bytes from src; rows at or past `rows` read as zeros) into
+// a [16][XS] LDS tile: each of the 4 waves moves 4 rows, one instruction per
+// row and 64-lane run of 16-byte chunks.
+template <int D, int XS>
+__device__ __forceinline__ void dma_rows_x4(const float *src, int rows, int row_bytes,
+                                            uint32_t base, int wave, int lane) {
+  const u32x4 rs = rsrc_words(src, (int64_t)rows * row_bytes);
+#pragma unroll
+  for (int part = 0; part < (D / 4 + 63) / 64; ++part) {
+    const int ch = part * 64 + lane;
+    if (ch < D / 4) {
+#pragma unroll
+      for (int n = 0; n < kX4Rows / 4; ++n) {
+        const int r = wave * (kX4Rows / 4) + n;
+        int32_t voff;
+        asm volatile("v_add_u32 %0, %1, %2" : "=v"(voff) : "s"(r * row_bytes), "v"(ch * 16));
+        lds_dma16(rs, base + (r * XS + part * 256) * 4, voff);
+      }
+    }
+  }
+}
+
+// The lane's Q = D/4 features [Q*lq, Q*lq + Q) of row `row` of one head of a
+// [T, H, D] fp32 tensor; rows outside the descriptor's range read as zeros.
+template <int D>
+__device__ __forceinline__ void load_row_quarter(float (&dst)[D / 4], rsrc_t r,
+                                                 int row_byte_off, int lq) {
+  constexpr int Q = D / 4;
+#pragma unroll
+  for (int i4 = 0; i4 < Q / 4; ++i4) {
+    const f32x4 v = __builtin_bit_cast(f32x4, buf_load16(r, row_byte_off + (Q * lq + 4 * i4) * 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[4 * i4 + e] = v[e];
+  }
+}
+
+__device__ __forceinline__ f32x4 mma4f(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// dQ, query-major over the forward's items (split items write scaled fp32
+// partial rows), 4 waves x 16 rows per pass (an item's rows in passes of
+// 64): per 16-key tile S^T = K Q^T, dP^T = V dO^T (K, V rows as A from LDS,
+// this lane's row quarter as B), P^T, dS^T, then dQ^T += K^T dS^T.
+template <int D>
+__global__ __launch_bounds__(256, 2) void varlen_dq_f32x4_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ part_dq,
+    const int32_t *__restrict__ items, int H, float c, float scale) {
+  using S = F32x4Smem<D>;
+  constexpr int Q = D / 4, NA = D / 64, XS = S::XS;
+  extern __shared__ __align__(16) float smem_x4[];
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int iq0 = it.v[0], q1 = it.v[1], k0 = it.v[2], k1 = it.v[3], pbase = it.v[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int row_bytes = H * D * 4;
+  const int nt = (k1 - k0 + kX4Rows - 1) / kX4Rows;
+  auto issue = [&](int kb, int buf) {
+    const int rows = uniform_clamp(k1 - kb, kX4Rows);
+    const int64_t off = ((int64_t)kb * H + h) * D;
+    float *base = smem_x4 + buf * S::kBuf;
+    dma_rows_x4<D, XS>(k + off, rows, row_bytes, lds_addr(base), wave, lane);
+    dma_rows_x4<D, XS>(v + off, rows, row_bytes, lds_addr(base + S::kTile), wave, lane);
+  };
+  for (int q0 = iq0; q0 < q1; q0 += 4 * kX4Rows) {
+    const int qrow = q0 + wave * kX4Rows + l16;
+    const bool row_ok = qrow < q1;
+    const bool wave_active = q0 + wave * kX4Rows < q1;
+    if (nt > 0) issue(k0, 0);
+    float qf[Q], gf[Q];
+    {
+      const int64_t nb = (int64_t)(q1 - q0) * row_bytes;
+      const int64_t off = ((int64_t)q0 * H + h) * D;
+      const int roff = (wave * kX4Rows + l16) * row_bytes;
+      load_row_quarter<D>(qf, make_rsrc(q + off, nb), roff, lq);
+      load_row_quarter<D>(gf, make_rsrc(dout + off, nb), roff, lq);
+    }
+    const float L = row_ok ? lse[(int64_t)qrow * H + h] : 0.f;
+    const float dl = row_ok ? delta[(int64_t)qrow * H + h] : 0.f;
+    f32x4 acc[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < nt; ++j) {
+      wait_vmcnt<0>();
+      __syncthreads();  // tile j landed; every wave is done with the other buffer
+      if (j + 1 < nt) issue(k0 + (j + 1) * kX4Rows, (j + 1) & 1);
+      const int kb = k0 + j * kX4Rows;
+      if (wave_active) {
+        const float *ks = smem_x4 + (j & 1) * S::kBuf;
+        const float *vs = ks + S::kTile;
+        // S^T, dP^T (16 keys x 16 rows): lane holds key kb + 4*lq + r of its row
+        f32x4 s2[2], dp2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) s2[e] = dp2[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float *ka = ks + l16 * XS + Q * lq;
+        const float *va = vs + l16 * XS + Q * lq;
+#pragma unroll
+        for (int i4 = 0; i4 < Q / 4; ++i4) {
+          const f32x4 kv = *reinterpret_cast<const f32x4 *>(ka + 4 * i4);
+          const f32x4 vv = *reinterpret_cast<const f32x4 *>(va + 4 * i4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s2[e & 1] = mma4f(kv[e], qf[4 * i4 + e], s2[e & 1]);
+            dp2[e & 1] = mma4f(vv[e], gf[4 * i4 + e], dp2[e & 1]);
+          }
+        }
+        const f32x4 s = s2[0] + s2[1], dp = dp2[0] + dp2[1];
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool kin = kb + 4 * lq + r < k1;
+          const float p = kin ? fast_exp2(__builtin_fmaf(s[r], c, -L)) : 0.f;
+          ds[r] = p * (dp[r] - dl);
+        }
+        // dQ^T += K^T dS^T over the tile's 16 keys (slot lq <-> key 4*lq + j4)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const float *kt = ks + (4 * lq + j4) * XS + 4 * l16;
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            const f32x4 kv = *reinterpret_cast<const f32x4 *>(kt + 64 * a);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc[a][b] = mma4f(kv[b], ds[j4], acc[a][b]);
+          }
+        }
+      }
+    }
+    if (row_ok) {
+      // lane: row qrow, features 64a + 16*lq + 4r + b
+      float *orow = pbase < 0 ? dq + ((int64_t)qrow * H + h) * D
+                              : part_dq + ((int64_t)(pbase + (qrow - iq0)) * H + h) * D;
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          f32x4 w;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) w[b] = acc[a][b][r] * scale;
+          *reinterpret_cast<f32x4 *>(orow + 64 * a + 16 * lq + 4 * r) = w;
+        }
+    }
+    __syncthreads();  // the next pass's first DMA overwrites buffer 0
+  }
+}
+
+// dK/dV, key-major over the plan's key tiles, 4 waves x 16 keys per pass (an
+// item's keys in passes of 64): per 16-row query block (Q, dO rows, LSE and
+// delta in LDS) S = Q K^T, dP = dO V^T (Q, dO rows as A, this lane's key
+// quarter as B), P = exp2(S c - LSE), dS = P (dP - delta), then
+// dV^T += dO^T P and dK^T += Q^T dS.  Rows past the segment arrive as zero Q
+// and dO rows, so both products vanish for them.
+template <int D>
+__global__ __launch_bounds__(256, 1) void varlen_dkv_f32x4_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv,
+    const int32_t *__restrict__ items, int H, float c, float scale) {
+  using S = F32x4Smem<D>;
+  constexpr int Q = D / 4, NA = D / 64, XS = S::XS;
+  extern __shared__ __align__(16) float smem_x4[];
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
+  const PlanItem it = load_item(items, item);
+  const int kt0 = it.v[0], kt1 = it.v[1], q0 = it.v[2], q1 = it.v[3];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int row_bytes = H * D * 4;
+  const int nb = (q1 - q0 + kX4Rows - 1) / kX4Rows;
+  // block qb: Q and dO rows, then LSE (waves 0, 2) and delta (waves 1, 3:
+  // the pairs write the same bytes), one 4-byte DMA per lane < 16
+  auto issue = [&](int qb, int buf) {
+    const int rows = uniform_clamp(q1 - qb, kX4Rows);
+    const int64_t off = ((int64_t)qb * H + h) * D;
+    float *base = smem_x4 + buf * S::kBuf;
+    dma_rows_x4<D, XS>(q + off, rows, row_bytes, lds_addr(base), wave, lane);
+    dma_rows_x4<D, XS>(dout + off, rows, row_bytes, lds_addr(base + S::kTile), wave, lane);
+    const float *vec = (wave & 1) ? delta : lse;
+    const u32x4 rv = rsrc_words32(vec + (int64_t)qb * H + h, (uint32_t)(rows * H * 4));
+    if (lane < kX4Rows)
+      lds_dma4(rv, lds_addr(base + 2 * S::kTile + (wave & 1) * kX4Rows), lane * H * 4);
+  };
+  for (int k0 = kt0; k0 < kt1; k0 += 4 * kX4Rows) {
+    const int key = k0 + wave * kX4Rows + l16;
+    const bool key_ok = key < kt1;
+    const bool wave_active = k0 + wave * kX4Rows < kt1;
+    if (nb > 0) issue(q0, 0);
+    float kf[Q], vf[Q];
+    {
+      const int64_t nbk = (int64_t)(kt1 - k0) * row_bytes;
+      const int64_t off = ((int64_t)k0 * H + h) * D;
+      const int roff = (wave * kX4Rows + l16) * row_bytes;
+      load_row_quarter<D>(kf, make_rsrc(k + off, nbk), roff, lq);
+      load_row_quarter<D>(vf, make_rsrc(v + off, nbk), roff, lq);
+    }
+    f32x4 adk[NA][4], adv[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) adk[a][b] = adv[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < nb; ++j) {
+      wait_vmcnt<0>();
+      __syncthreads();  // block j landed; every wave is done with the other buffer
+      if (j + 1 < nb) issue(q0 + (j + 1) * kX4Rows, (j + 1) & 1);
+      if (wave_active) {
+        const float *qs = smem_x4 + (j & 1) * S::kBuf;
+        const float *gs = qs + S::kTile;
+        const float *ls = qs + 2 * S::kTile;
+        // S, dP (16 rows x 16 keys): lane holds row 4*lq + r of the block for its key
+        f32x4 s2[2], dp2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) s2[e] = dp2[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float *qa = qs + l16 * XS + Q * lq;
+        const float *ga = gs + l16 * XS + Q * lq;
+#pragma unroll
+        for (int i4 = 0; i4 < Q / 4; ++i4) {
+          const f32x4 qv = *reinterpret_cast<const f32x4 *>(qa + 4 * i4);
+          const f32x4 gv = *reinterpret_cast<const f32x4 *>(ga + 4 * i4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s2[e & 1] = mma4f(qv[e], kf[4 * i4 + e], s2[e & 1]);
+            dp2[e & 1] = mma4f(gv[e], vf[4 * i4 + e], dp2[e & 1]);
+          }
+        }
+        const f32x4 s = s2[0] + s2[1], dp = dp2[0] + dp2[1];
+        const f32x4 L4 = *reinterpret_cast<const f32x4 *>(ls + 4 * lq);
+        const f32x4 D4 = *reinterpret_cast<const f32x4 *>(ls + kX4Rows + 4 * lq);
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = fast_exp2(__builtin_fmaf(s[r], c, -L4[r]));
+          ds[r] = p[r] * (dp[r] - D4[r]);
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS over the block's 16 rows (slot lq <-> row 4*lq + j4)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const float *gt = gs + (4 * lq + j4) * XS + 4 * l16;
+          const float *qt = qs + (4 * lq + j4) * XS + 4 * l16;
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            const f32x4 gv = *reinterpret_cast<const f32x4 *>(gt + 64 * a);
+            const f32x4 qv = *reinterpret_cast<const f32x4 *>(qt + 64 * a);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              adv[a][b] = mma4f(gv[b], p[j4], adv[a][b]);
+              adk[a][b] = mma4f(qv[b], ds[j4], adk[a][b]);
+            }
+          }
+        }
+      }
+    }
+    if (key_ok) {
+      // lane: key `key`, features 64a + 16*lq + 4r + b
+      float *krow = dk + ((int64_t)key * H + h) * D;
+      float *vrow = dv + ((int64_t)key * H + h) * D;
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          f32x4 wk, wv;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            wk[b] = adk[a][b][r] * scale;
+            wv[b] = adv[a][b][r];
+          }
+          const int f = 64 * a + 16 * lq + 4 * r;
+          *reinterpret_cast<f32x4 *>(krow + f) = wk;
+          *reinterpret_cast<f32x4 *>(vrow + f) = wv;
+        }
+    }
+    __syncthreads();  // the next pass's first DMA overwrites buffer 0
+  }
+}
+
+template <int D>
+void launch_dq_f32x4(const VarlenArgs &a, hipStream_t st) {
+  const int smem = F32x4Smem<D>::kBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dq_f32x4_kernel<D>), smem);
+  hipLaunchKernelGGL((varlen_dq_f32x4_kernel<D>), dim3((unsigned)(a.n_items * a.H)), dim3(256),
+                     smem, st, (const float *)a.q, (const float *)a.k, (const float *)a.v,
+                     (const float *)a.dout, a.lse_in, a.delta, (float *)a.dq, a.part_o, a.items,
+                     a.H, a.scale * kLog2e, a.scale);
+}
+
+template <int D>
+void launch_dkv_f32x4(const VarlenArgs &a, hipStream_t st) {
+  const int smem = F32x4Smem<D>::kBytes;
+  allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dkv_f32x4_kernel<D>), smem);
+  hipLaunchKernelGGL((varlen_dkv_f32x4_kernel<D>), dim3((unsigned)(a.n_kv * a.H)), dim3(256),
+                     smem, st, (const float *)a.q, (const float *)a.k, (const float *)a.v,
+                     (const float *)a.dout, a.lse_in, a.delta, (float *)a.dk, (float *)a.dv,
+                     a.kv_items, a.H, a.scale * kLog2e, a.scale);
+}
+
 template <int D, int NW>
 void launch_dq_f32_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = F32DqSmem<D>::kBytes;
@@ -642,7 +972,7 @@ void launch_dkv_f32_nw(const VarlenArgs &a, hipStream_t st) {
 }  // namespace
 
 bool f32_varlen_mfma_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
-bool f32_varlen_bwd_mfma_d(int D) { return D == 32 || D == 64 || D == 128; }
+bool f32_varlen_bwd_mfma_d(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
 void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
   if (a.n_items == 0) return;
@@ -651,6 +981,7 @@ void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
     case 32: wide ? launch_dq_f32_nw<32, 8>(a, st) : launch_dq_f32_nw<32, 4>(a, st); break;
     case 64: wide ? launch_dq_f32_nw<64, 8>(a, st) : launch_dq_f32_nw<64, 4>(a, st); break;
     case 128: launch_dq_f32_nw<128, 4>(a, st); break;  // walks 256-row items in halves
+    case 256: launch_dq_f32x4<256>(a, st); break;
     default: break;
   }
 }
@@ -663,6 +994,7 @@ void launch_f32_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
     case 32: launch_dkv_f32_nw<32, 4>(a, st); break;
     case 64: launch_dkv_f32_nw<64, 4>(a, st); break;
     case 128: launch_dkv_f32_nw<128, 4>(a, st); break;
+    case 256: launch_dkv_f32x4<256>(a, st); break;
     default: break;
   }
 }

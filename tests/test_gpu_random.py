@@ -6,12 +6,20 @@ the public entry points (C ABI underneath) and checks every output and
 gradient with the parity bounds of tests/parity.py.  The shapes cover the
 matrix-core paths' edges: tails of every tile size, split and unsplit key
 ranges, head counts that do not divide 64, widths that are padded.
+
+Varlen gradients in 16-bit are held to the reference algorithm's own error
+(assert_within_reference_numerics): a segment with a handful of keys against
+hundreds of queries gives those keys dK / dV sums of magnitude ~10 (bf16
+spacing 0.0625 there) over P and dS that the reference rounds to bf16 before
+the products (fa/kernels.py:345, 480, 489), while rms(ref) stays below 1, so
+neither the floor-subtracted nor the rms-relative form of the absolute bound
+applies to them.
 """
 import numpy as np
 import pytest
 import torch
 
-from parity import assert_close
+from parity import assert_close, assert_within_reference_numerics
 from test_gpu_absorb import NAMES as ABSORB_NAMES
 from test_gpu_absorb import run_case as absorb_case
 from test_gpu_varlen import run_case as varlen_case
@@ -34,13 +42,19 @@ def _varlen_draw(seed):
     return q, k, H, D, dt
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_varlen_random_shapes(device, seed):
     q, k, H, D, dt = _varlen_draw(seed)
     print(f"[varlen random {seed}] q={q} k={k} H={H} D={D} {dt}", flush=True)
-    got, ref = varlen_case(q, k, H, D, dt, device, seed=seed)
-    for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
-        assert_close(n, a, r)
+    if dt == torch.float32:
+        got, ref = varlen_case(q, k, H, D, dt, device, seed=seed)
+        for n, a, r in zip(("o", "dq", "dk", "dv"), got, ref):
+            assert_close(n, a, r)
+        return
+    got, ref, emul = varlen_case(q, k, H, D, dt, device, seed=seed, reference_numerics=True)
+    assert_close("o", got[0], ref[0])
+    for n, a, r, em in zip(("dq", "dk", "dv"), got[1:], ref[1:], emul):
+        assert_within_reference_numerics(n, a, r, em)
 
 
 def _absorb_draw(seed):
@@ -55,7 +69,7 @@ def _absorb_draw(seed):
     return q, k, H, D_H, d_kv, dt
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_absorb_random_shapes(device, seed):
     q, k, H, D_H, d_kv, dt = _absorb_draw(seed)
     print(f"[absorb random {seed}] q={q} k={k} H={H} D_H={D_H} d_kv={d_kv} {dt}", flush=True)

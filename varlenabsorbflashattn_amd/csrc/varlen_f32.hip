@@ -245,10 +245,9 @@ void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward (D in {32, 64, 128}; D = 256 below, on 16x16x4 products).  At
-// D = 128 the operands held in registers and the accumulators take more than
-// half the register file, so those workgroups run one wave per SIMD; at
-// D = 256 they would not fit at all.
+// Backward at D in {32, 64} (D = 128 and 256 below, on 16x16x4 products:
+// here the operands held in registers and the accumulators would take more
+// than half the register file at D = 128 and more than all of it at 256).
 //
 // dQ, query-major over the forward's items (split items write scaled fp32
 // partial rows that the ordered sum adds): per 32-key tile
@@ -257,8 +256,8 @@ void launch_fwd_f32_d(const VarlenArgs &a, hipStream_t st) {
 //   P^T = exp2(S^T c - LSE), dS^T = P^T (dP^T - delta)   (lane = query row)
 //   dQ^T += K^T dS^T                 (K^T staged transposed; step s takes the
 //                                    keys of S^T's element s, as the forward's PV)
-// An item's rows are walked 32*NW at a time, so a 256-row item also runs on
-// four waves (D = 128) by streaming its key range twice.
+// An item's rows are walked 32*NW at a time (one pass for the items the plan
+// gives these head dims).
 // ---------------------------------------------------------------------------
 template <int D>
 struct F32DqSmem {
@@ -621,9 +620,11 @@ __global__ __launch_bounds__(64 * NW, NW == 8 || D >= 128 ? 1 : 2) void varlen_d
 }
 
 // ---------------------------------------------------------------------------
-// Backward at D = 256 on v_mfma_f32_16x16x4_f32.  The 32x32x2 kernels above
-// hold a row's (or key's) whole Q^T / dO^T (or K^T / V^T) operands, 2 * D/2
-// floats, beside D/32 accumulator tiles: 512 registers and more at D = 256.
+// Backward at D in {128, 256} on v_mfma_f32_16x16x4_f32.  The 32x32x2
+// kernels above hold a row's (or key's) whole Q^T / dO^T (or K^T / V^T)
+// operands, 2 * D/2 floats, beside D/32 accumulator tiles: 512 registers and
+// more at D = 256; at D = 128 they fit at one wave per SIMD, 4.4% slower
+// than these kernels on C2's lengths (fp32 fwd+bwd 20.96 against 20.04 ms).
 // With 16 rows (keys) per wave each lane group lq holds only the quarter of
 // the features it reduces over (Q = D/4 per operand), as the fp32 absorb
 // kernels do:
@@ -980,20 +981,21 @@ void launch_f32_varlen_dq(const VarlenArgs &a, hipStream_t st) {
   switch (a.D) {
     case 32: wide ? launch_dq_f32_nw<32, 8>(a, st) : launch_dq_f32_nw<32, 4>(a, st); break;
     case 64: wide ? launch_dq_f32_nw<64, 8>(a, st) : launch_dq_f32_nw<64, 4>(a, st); break;
-    case 128: launch_dq_f32_nw<128, 4>(a, st); break;  // walks 256-row items in halves
+    case 128: launch_dq_f32x4<128>(a, st); break;
     case 256: launch_dq_f32x4<256>(a, st); break;
     default: break;
   }
 }
 
-// Key tiles of the plan on 4 waves; the kernel walks longer items (256-key
-// tiles at D = 128, fused-planned chunks at D <= 64) in 128-key steps.
+// Key tiles of the plan on 4 waves; the 32x32x2 kernel walks longer items
+// (fused-planned chunks at D <= 64) in 128-key steps, the 16x16x4 kernel any
+// item in 64-key steps.
 void launch_f32_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
   switch (a.D) {
     case 32: launch_dkv_f32_nw<32, 4>(a, st); break;
     case 64: launch_dkv_f32_nw<64, 4>(a, st); break;
-    case 128: launch_dkv_f32_nw<128, 4>(a, st); break;
+    case 128: launch_dkv_f32x4<128>(a, st); break;
     case 256: launch_dkv_f32x4<256>(a, st); break;
     default: break;
   }

@@ -104,6 +104,90 @@ __device__ __forceinline__ typename Mfma<T>::v8 tr_operand(const T *tile, int st
   return as_v8<T>(join(lo, hi));
 }
 
+// ---- row stores of transposed accumulators -------------------------------
+// A wave's output block of 32 rows x 32*NDT columns held as NDT transposed
+// 32x32 accumulators (acc[i] = columns 32i .. 32i+31 as C rows, the 32
+// output rows as C columns): lane l holds row l % 32 at columns
+// 32i + 8g + 4(l/32) + e, g, e < 4.  Stored straight from the registers,
+// every instruction writes 16 (or, for fp32, 32) bytes into each of 32 rows.
+// StagedRows sends the block through the wave's own LDS region instead, so
+// every store instruction writes whole rows, 16 bytes per lane.
+template <typename O, int NDT>
+struct StagedRows {
+  static constexpr int kW = 32 * NDT;                        // columns
+  // row stride: 16-byte aligned for the row reads, 16 bytes of padding
+  static constexpr int kStride = kW * (int)sizeof(O) + 16;   // bytes
+  static constexpr int kBytes = 32 * kStride;                // per wave
+  static constexpr int kLanesPerRow = kW * (int)sizeof(O) / 16;
+  static constexpr int kRowsPerStep = 64 / kLanesPerRow;
+
+  // Writes conv(acc) into `stage` (kBytes, this wave's), then stores row r
+  // of the block at out + r * row_stride (elements) for r < rows.  The caller
+  // makes `stage` free of other waves' accesses; LDS operations of one wave
+  // execute in order, so the reads see this wave's writes.  The lane index is
+  // formed here (mbcnt), not taken from the kernel's, so that nothing of the
+  // epilogue's addressing is computed ahead of a kernel's main loop and held
+  // in registers across it.
+  template <typename F>
+  static __device__ __forceinline__ void store(const f32x16 (&acc)[NDT], F conv,
+                                               unsigned char *stage, O *out,
+                                               int64_t row_stride, int rows) {
+    static_assert(kLanesPerRow >= 1 && kLanesPerRow <= 64 && 64 % kLanesPerRow == 0,
+                  "row width");
+    const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int r = lane & 31, hf = lane >> 5;
+    typedef __attribute__((__vector_size__(4 * sizeof(O)))) O O4;
+#pragma unroll
+    for (int i = 0; i < NDT; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        O4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = conv(acc[i][g * 4 + e]);
+        *reinterpret_cast<O4 *>(stage + r * kStride + (32 * i + 8 * g + 4 * hf) * sizeof(O)) = w;
+      }
+    asm volatile("" ::: "memory");
+    const int c = lane % kLanesPerRow, r0 = lane / kLanesPerRow;
+#pragma unroll
+    for (int s = 0; s < 32 / kRowsPerStep; ++s) {
+      const int rr = s * kRowsPerStep + r0;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + rr * kStride + c * 16);
+      if (rr < rows)
+        *reinterpret_cast<u32x4 *>(out + rr * row_stride + c * (16 / (int)sizeof(O))) = v;
+    }
+    asm volatile("" ::: "memory");
+  }
+};
+
+// A wave's block as 16-bit rows (one pass) or as fp32 rows (split partials:
+// two passes over column halves when there are two or more column tiles), in
+// a per-wave region of kBytes.
+template <typename T, int ND>
+struct RowStore {
+  using R16 = StagedRows<T, ND>;
+  static constexpr int kHalves = ND % 2 == 0 ? 2 : 1;
+  using R32 = StagedRows<float, ND / kHalves>;
+  static constexpr int kBytes = R16::kBytes > R32::kBytes ? R16::kBytes : R32::kBytes;
+
+  template <typename F>
+  static __device__ __forceinline__ void rows16(const f32x16 (&acc)[ND], F conv,
+                                                unsigned char *stage, T *out,
+                                                int64_t row_stride, int rows) {
+    R16::store(acc, conv, stage, out, row_stride, rows);
+  }
+  // fp32 rows of acc * mul
+  static __device__ __forceinline__ void rows32(const f32x16 (&acc)[ND], float mul,
+                                                unsigned char *stage, float *out,
+                                                int64_t row_stride, int rows) {
+    constexpr int NH = ND / kHalves;
+#pragma unroll
+    for (int hh = 0; hh < kHalves; ++hh)
+      R32::store(*reinterpret_cast<const f32x16(*)[NH]>(&acc[hh * NH]),
+                 [&](float x) { return x * mul; }, stage, out + hh * NH * 32, row_stride,
+                 rows);
+  }
+};
+
 // 16-bit element e (0..7) of a 16-byte chunk.
 __device__ __forceinline__ uint32_t half_of(const u32x4 &x, int e) {
   return (x[e >> 1] >> ((e & 1) * 16)) & 0xffffu;

@@ -73,6 +73,15 @@ struct DkvSmem {
   static constexpr int kBytes = 2 * kBufBytes + 1024;
 };
 
+// Dynamic LDS of the dK/dV kernel: the query-block buffers, or the per-wave
+// row-store regions of the epilogue if those are larger (D = 128 on 8 waves).
+template <typename T, int D, int NW>
+constexpr int dkv_lds_bytes() {
+  constexpr int kNDO = D / 32 / (D >= 256 ? 2 : 1);
+  constexpr int kStage = NW * StagedRows<T, kNDO>::kBytes;
+  return DkvSmem<D>::kBytes > kStage ? DkvSmem<D>::kBytes : kStage;
+}
+
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
 // past r_end read as zero) into a GTile block: wave w of NW moves
 // rows RPW*w .. RPW*w + RPW-1 (RPW = 32/NW), one instruction per row with
@@ -165,8 +174,6 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const int key = k0 + wave * 32 + lrow;
-  const bool key_ok = key < k1;
   const bool wave_active = k0 + wave * 32 < k1;
 
   // stage query block qb: Q and dO rows by 16-byte DMA, LSE and delta (strided
@@ -360,24 +367,20 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   }
   wait_vmcnt<0>();
 
-  if (!key_ok) return;
-  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-  T *dkr = dk + ((int64_t)key * H + h) * D;
-  T *dvr = dv + ((int64_t)key * H + h) * D;
-#pragma unroll
-  for (int dtile = 0; dtile < NDO; ++dtile)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      T4 wk, wv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        wk[e] = static_cast<T>(adk[dtile][g * 4 + e] * scale);
-        wv[e] = static_cast<T>(adv[dtile][g * 4 + e]);
-      }
-      const int d = (dpart * NDO + dtile) * 32 + g * 8 + lhalf * 4;
-      *reinterpret_cast<T4 *>(dkr + d) = wk;
-      *reinterpret_cast<T4 *>(dvr + d) = wv;
-    }
+  // dK and dV leave as whole rows through per-wave LDS regions (over the
+  // query-block buffers, free once every wave is past its last block):
+  // stored from the accumulators, every instruction wrote 16 bytes into each
+  // of 32 rows, which cost 14% of the kernel on the stage-1 replay shapes.
+  __syncthreads();
+  if (!wave_active) return;
+  using SR = StagedRows<T, NDO>;
+  unsigned char *stage = smem_raw + wave * SR::kBytes;
+  const int rows = uniform_clamp(k1 - (k0 + wave * 32), 32);
+  const int64_t off = ((int64_t)(k0 + wave * 32) * H + h) * D + dpart * NDO * 32;
+  SR::store(adk, [&](float x) { return static_cast<T>(x * scale); }, stage, dk + off,
+            (int64_t)H * D, rows);
+  SR::store(adv, [](float x) { return static_cast<T>(x); }, stage, dv + off, (int64_t)H * D,
+            rows);
 }
 
 // Fused K-major dQ/dK/dV for segments with at most kFusedMaxQ (<= 32)
@@ -894,38 +897,26 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dq_kernel(
     if (j < nblk) block(j, std::true_type{}, j & 1);
   }
 
-  if (!row_ok) return;
-  if (pbase < 0) {
-    typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-    T *row = dq + ((int64_t)qrow * H + h) * D;
-#pragma unroll
-    for (int dtile = 0; dtile < ND; ++dtile)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        T4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[dtile][g * 4 + e] * scale);
-        *reinterpret_cast<T4 *>(row + dtile * 32 + g * 8 + lhalf * 4) = w;
-      }
-  } else {
-    float *row = part_dq + ((int64_t)(pbase + qrow - q0) * H + h) * D;
-#pragma unroll
-    for (int dtile = 0; dtile < ND; ++dtile)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = acc[dtile][g * 4 + e] * scale;
-        *reinterpret_cast<f32x4 *>(row + dtile * 32 + g * 8 + lhalf * 4) = w;
-      }
-  }
+  if (!wave_active) return;
+  // dQ (or a split's fp32 partial rows) leaves as whole rows through the
+  // wave's LDS region (the K/V buffers, free after the loop's last barrier);
+  // stored from the accumulators it cost 5% of the C2 dQ kernel.
+  using RS = RowStore<T, ND>;
+  unsigned char *stage = smem_raw + wave * RS::kBytes;
+  const int rows = uniform_clamp(q1 - (q0 + wave * 32), 32);
+  if (pbase < 0)
+    RS::rows16(acc, [&](float x) { return static_cast<T>(x * scale); }, stage,
+               dq + ((int64_t)(q0 + wave * 32) * H + h) * D, (int64_t)H * D, rows);
+  else
+    RS::rows32(acc, scale, stage, part_dq + ((int64_t)(pbase + wave * 32) * H + h) * D,
+               (int64_t)H * D, rows);
 }
 
 }  // namespace
 
 template <typename T, int D, int NW>
 void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
-  const int smem = DkvSmem<D>::kBytes;
+  const int smem = dkv_lds_bytes<T, D, NW>();
   allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, NW>), smem);
   const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
   hipLaunchKernelGGL((varlen_dkv_kernel<T, D, NW>),
@@ -956,9 +947,17 @@ void launch_mfma_varlen_fkv(const VarlenArgs &a, hipStream_t st) {
                      a.scale * kLog2e, a.scale, a.part_fq);
 }
 
+// Dynamic LDS of the dQ kernel: the K/V block buffers, or the per-wave
+// row-store regions of the epilogue if those are larger.
+template <typename T, int D, int NW>
+constexpr int dq_lds_bytes() {
+  constexpr int kStage = NW * RowStore<T, D / 32>::kBytes;
+  return DqSmem<D>::kBytes > kStage ? DqSmem<D>::kBytes : kStage;
+}
+
 template <typename T, int D, int NW>
 void launch_dq_nw(const VarlenArgs &a, hipStream_t st) {
-  const int smem = DqSmem<D>::kBytes;
+  const int smem = dq_lds_bytes<T, D, NW>();
   allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dq_kernel<T, D, NW>), smem);
   hipLaunchKernelGGL((varlen_dq_kernel<T, D, NW>), dim3((unsigned)(a.n_items * a.H)),
                      dim3(64 * NW), smem, st, (const T *)a.q, (const T *)a.k, (const T *)a.v,

@@ -304,44 +304,41 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_fwd_kernel(
     if (j + 1 < nt) step(j + 1, std::integral_constant<int, 1>{});
   }
 
-  if (!row_ok) return;
+  if (!wave_active) return;
   const float l = l_part + __shfl_xor(l_part, 32, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const float lse_v = l > 0.f ? m_run + fast_log2(l) : kNegInf;
+  // O (or a split's fp32 partial rows) leaves as whole rows through the
+  // wave's LDS region (the K/V buffers: every wave has passed the loop's last
+  // barrier).  Stored from the accumulators, every instruction wrote 8 or 16
+  // bytes into each of 32 rows, 8% of the C2 forward.
+  using RS = RowStore<T, ND>;
+  unsigned char *stage = smem_raw + wave * RS::kBytes;
+  const int rows = uniform_clamp(q1 - (q0 + wave * 32), 32);
   if (pbase < 0) {
-    T *orow = o + ((int64_t)qrow * H + h) * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T T4;
-        T4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(acc[dt][g * 4 + e] * inv);
-        *reinterpret_cast<T4 *>(orow + dt * 32 + g * 8 + lhalf * 4) = w;
-      }
-    if (lhalf == 0) lse[(int64_t)qrow * H + h] = lse_v;
+    RS::rows16(acc, [&](float x) { return static_cast<T>(x * inv); }, stage,
+               o + ((int64_t)(q0 + wave * 32) * H + h) * D, (int64_t)H * D, rows);
+    if (row_ok && lhalf == 0) lse[(int64_t)qrow * H + h] = lse_v;
   } else {
-    const int64_t prow = pbase + (qrow - q0);
-    float *orow = part_o + (prow * H + h) * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = acc[dt][g * 4 + e] * inv;
-        *reinterpret_cast<f32x4 *>(orow + dt * 32 + g * 8 + lhalf * 4) = w;
-      }
-    if (lhalf == 0) part_lse[prow * H + h] = lse_v;
+    const int64_t prow = pbase + wave * 32;
+    RS::rows32(acc, inv, stage, part_o + (prow * H + h) * D, (int64_t)H * D, rows);
+    if (row_ok && lhalf == 0) part_lse[(prow + lrow) * H + h] = lse_v;
   }
 }
 
 }  // namespace
 
+// Dynamic LDS of the forward: the K/V buffers, or the per-wave row-store
+// regions of the epilogue if those are larger.
+template <typename T, int D, int NW>
+constexpr int fwd_lds_bytes() {
+  constexpr int kStage = NW * RowStore<T, D / 32>::kBytes;
+  return FwdSmem<D>::kBytes > kStage ? FwdSmem<D>::kBytes : kStage;
+}
+
 template <typename T, int D, int NW>
 void launch_fwd_nw(const VarlenArgs &a, hipStream_t st) {
-  const int smem = FwdSmem<D>::kBytes;
+  const int smem = fwd_lds_bytes<T, D, NW>();
   allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_fwd_kernel<T, D, NW>), smem);
   const int64_t n_wg = a.xcd_heads ? (a.n_items + kXcds - 1) / kXcds * kXcds * a.H
                                    : a.n_items * a.H;

@@ -166,12 +166,19 @@ def bench_varlen_fp32(steps):
 
 
 def varlen_line(case, step_st, fwd_st):
+    """TFLOP/s on the FA2 convention (forward 4, backward 10 H D sum(Lq Lk));
+    for 16-bit inputs also as fractions of the 2.5 PFLOP/s bf16/fp16 peak
+    (the backward: step mean minus forward mean)."""
     tot = case.flops_fwd + case.flops_bwd
-    return {"sum_L_q": int(sum(case.q_lens)), "sum_L_k": int(sum(case.k_lens)),
+    line = {"sum_L_q": int(sum(case.q_lens)), "sum_L_k": int(sum(case.k_lens)),
             "n_seq": len(case.q_lens), "H": case.H, "D": case.D,
             "fwd_bwd_ms": step_st, "fwd_bwd_TFLOP/s": tot / (step_st["mean"] * 1e-3) / 1e12,
             "fwd_ms": fwd_st, "fwd_TFLOP/s": case.flops_fwd / (fwd_st["mean"] * 1e-3) / 1e12,
             "bwd_TFLOP/s": case.flops_bwd / ((step_st["mean"] - fwd_st["mean"]) * 1e-3) / 1e12}
+    if str(case.dtype) in ("torch.bfloat16", "torch.float16"):
+        for key in ("fwd_bwd", "fwd", "bwd"):
+            line[key + "_frac"] = line[key + "_TFLOP/s"] / BF16_PEAK_TFLOPS
+    return line
 
 
 def fused_case():

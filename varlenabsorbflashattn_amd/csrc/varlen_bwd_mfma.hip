@@ -403,9 +403,12 @@ struct FusedSmem {
   static constexpr int kQOff = 0;                     // Q block (GTile)
   static constexpr int kDoOff = kTile * 2;            // dO block (GTile)
   static constexpr int kLsOff = 2 * kTile * 2;        // LSE [32], delta [32]
-  static constexpr int kROff = kLsOff + 2 * kRB * 4;  // K rows (a GTile per wave), later the dQ^T sums
+  static constexpr int kROff = kLsOff + 2 * kRB * 4;  // K rows (a slot per wave), later the dQ^T sums
   static constexpr int kRS = D + 4;                   // fp32 row stride of the sums
-  static constexpr int kKtBytes = 4 * kTile * 2;
+  // a wave's slot: its K rows (GTile), after the tile's dQ^T products the
+  // dK / dV row-store region (StagedRows, 32 rows of D + 8 elements)
+  static constexpr int kSlot = kTile * 2 > 32 * (D * 2 + 16) ? kTile * 2 : 32 * (D * 2 + 16);
+  static constexpr int kKtBytes = 4 * kSlot;
   static constexpr int kRedBytes = 4 * 32 * kRS * 4;
   static constexpr int kDsS = 40;                     // dS^T [32 keys][40]
   static constexpr int kDsOff = kROff + (kKtBytes > kRedBytes ? kKtBytes : kRedBytes);
@@ -476,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
   const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(smem_raw + S::kQOff));
   const lds_cptr<T> ds_ = as_lds(reinterpret_cast<const T *>(smem_raw + S::kDoOff));
   const float *ls = reinterpret_cast<const float *>(smem_raw + S::kLsOff);
-  T *kt = reinterpret_cast<T *>(smem_raw + S::kROff) + wave * S::kTile;
+  T *kt = reinterpret_cast<T *>(smem_raw + S::kROff + wave * S::kSlot);
   T *dst = reinterpret_cast<T *>(smem_raw + S::kDsOff) + wave * 32 * S::kDsS;
   const int a_off = L::row(lrow) + lhalf * 8;
   const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
@@ -487,8 +490,8 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
 
   // one tile; false when this wave has no keys in it (nor in later tiles)
   auto tile = [&](int t) -> bool {
-    const int key = k0 + t * 128 + wave * 32 + lrow;
-    if (k0 + t * 128 + wave * 32 >= k1) return false;
+    const int kw = k0 + t * 128 + wave * 32;  // this wave's first key
+    if (kw >= k1) return false;
     // K rows to this wave's LDS rows, K^T operands of dQ^T read back
     // transposed (LDS operations of one wave execute in order)
 #pragma unroll
@@ -583,23 +586,19 @@ __global__ __launch_bounds__(256, 2) void varlen_fkv_kernel(
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) dqa[dt] = M::mma(ktf[hk * ND + dt], b, dqa[dt]);
     }
-    if (key < k1) {
-      T *dkr = dk + ((int64_t)key * H + h) * D;
-      T *dvr = dv + ((int64_t)key * H + h) * D;
-#pragma unroll
-      for (int dtile = 0; dtile < ND; ++dtile)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          T4 wk, wv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            wk[e] = static_cast<T>(adk[dtile][g * 4 + e] * scale);
-            wv[e] = static_cast<T>(adv[dtile][g * 4 + e]);
-          }
-          const int d = dtile * 32 + g * 8 + lhalf * 4;
-          *reinterpret_cast<T4 *>(dkr + d) = wk;
-          *reinterpret_cast<T4 *>(dvr + d) = wv;
-        }
+    // dK / dV leave as whole rows through the wave's slot (its K rows were
+    // read into ktf at the top of the tile; LDS operations of one wave
+    // execute in order)
+    {
+      using SR = StagedRows<T, ND>;
+      static_assert(SR::kBytes <= S::kSlot, "row-store region");
+      const int64_t off = ((int64_t)kw * H + h) * D;
+      const int rows = uniform_clamp(k1 - kw, 32);
+      unsigned char *stage = reinterpret_cast<unsigned char *>(kt);
+      SR::store(adk, [&](float x) { return static_cast<T>(x * scale); }, stage, dk + off,
+                (int64_t)H * D, rows);
+      SR::store(adv, [](float x) { return static_cast<T>(x); }, stage, dv + off,
+                (int64_t)H * D, rows);
     }
     return true;
   };

@@ -477,7 +477,6 @@ __global__ __launch_bounds__(64 * kDxWaves, FP > kMaxF ? 1 : 2) void absorb_dx_r
   for (int st = 0; st < nsub; ++st) {
     const int kb = d.k0 + st * D::kSub;
     if (kb + d.wave * 32 >= d.k1) break;  // wave-uniform: no keys left for this wave
-    const int key = kb + d.wave * 32 + d.lrow;
     v8 pb[2][2], sb[2][2];
     d.template block_p_ds<kPre>(xf, 0, c, scale, pb[0], sb[0]);
     if (nblk > 1) d.template block_p_ds<kPre>(xf, 1, c, scale, pb[1], sb[1]);

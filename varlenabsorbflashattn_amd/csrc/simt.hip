@@ -262,10 +262,10 @@ __global__ __launch_bounds__(256) void simt_absorb_fwd(
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void simt_absorb_du(
-    const T *__restrict__ u, const T *__restrict__ X, const T *__restrict__ wv,
-    const T *__restrict__ dO, const float *__restrict__ lse, const float *__restrict__ delta,
-    T *__restrict__ du, const T *__restrict__ dax_ws, float *__restrict__ ax_ws,
-    const int32_t *__restrict__ cu_items, int H, int F, int DH, float c, float scale) {
+    const T *__restrict__ u, const T *__restrict__ X, const float *__restrict__ lse,
+    const float *__restrict__ delta, T *__restrict__ du, const T *__restrict__ dax_ws,
+    float *__restrict__ ax_ws, const int32_t *__restrict__ cu_items, int H, int F, float c,
+    float scale) {
   // cu_items: one item per token tile, {t0, t1, k0, k1}: the segment's keys.
   const PlanItem it = load_item(cu_items, blockIdx.x);
   const int t0 = it.v[0], t1 = it.v[1], k0 = it.v[2], k1 = it.v[3];
@@ -402,9 +402,8 @@ template <typename T>
 void launch_simt_absorb_du(const AbsorbArgs &a, hipStream_t st) {
   if (a.n_qseg == 0) return;
   hipLaunchKernelGGL(simt_absorb_du<T>, dim3(a.n_qseg), dim3(256), 0, st, (const T *)a.u,
-                     (const T *)a.X, (const T *)a.wv, (const T *)a.dO, a.lse_in, a.delta,
-                     (T *)a.du, (const T *)a.dax, a.ax, a.qseg_items, a.H, a.F, a.DH, a.scale * kLog2e,
-                     a.scale);
+                     (const T *)a.X, a.lse_in, a.delta, (T *)a.du, (const T *)a.dax, a.ax,
+                     a.qseg_items, a.H, a.F, a.scale * kLog2e, a.scale);
 }
 
 template <typename T>

@@ -79,7 +79,9 @@ template <typename T, int D, int NW>
 constexpr int dkv_lds_bytes() {
   constexpr int kNDO = D / 32 / (D >= 256 ? 2 : 1);
   constexpr int kStage = NW * StagedRows<T, kNDO>::kBytes;
-  return DkvSmem<D>::kBytes > kStage ? DkvSmem<D>::kBytes : kStage;
+  constexpr int kBase = DkvSmem<D>::kBytes > kStage ? DkvSmem<D>::kBytes : kStage;
+  // D = 256: the partial S / dP exchange region after the query-block buffers
+  return D >= 256 ? DkvSmem<D>::kBytes + NW * 64 * 32 * 4 : kBase;
 }
 
 // LDS-DMA of one head's rows [r0, r0 + 32) of a [T, H, D] tensor (rows at or
@@ -148,7 +150,7 @@ __device__ __forceinline__ void dma_block_rows(const T *src, int r0, int r_end, 
 }
 
 template <typename T, int D, int NW>
-__global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
+__global__ __launch_bounds__(64 * NW, D >= 256 && NW < 8 ? 1 : 2) void varlen_dkv_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     const T *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
     T *__restrict__ dk, T *__restrict__ dv, const int32_t *__restrict__ items, int H, float c,
@@ -156,25 +158,28 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   using M = Mfma<T>;
   using S = DkvSmem<D>;
   using L = GTile<D>;
-  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int ND = D / 32;
   constexpr int kPre = D >= 128 ? 2 : 4;  // operand ring depth within the register budget
-  // At D=256 two workgroups share a key tile, each accumulating dK/dV for one
-  // half of d (S and dP still over all of d): the full-width accumulators did
-  // not fit beside the K/V operands and spilled.
-  constexpr int kDsplit = D >= 256 ? 2 : 1;
-  constexpr int NDO = ND / kDsplit;  // 32-wide d tiles of dK/dV per workgroup
+  // At D = 256 (8 waves) waves w and w + 4 share 32 keys, each holding K / V
+  // and accumulating dK / dV for one half of d: each forms S and dP over its
+  // half, the two partial sums meet through LDS, and both form the same P
+  // and dS (full-width K / V operands beside the accumulators would not fit).
+  constexpr bool kShare = D >= 256;
+  static_assert(!kShare || NW == 8, "D = 256 runs on 8 waves");
+  constexpr int NDO = kShare ? ND / 2 : ND;  // 32-wide d tiles of dK/dV per wave
+  constexpr int NCS = 2 * NDO;               // 16-wide d chunks of the S / dP products
   constexpr bool kDeltaInChain = D <= 64;
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
-  const int dpart = kDsplit > 1 ? (int)(blockIdx.x % kDsplit) : 0;
-  const int bid = blockIdx.x / kDsplit;
-  const int item = bid / H, h = bid % H;
+  const int item = blockIdx.x / H, h = blockIdx.x % H;
   const PlanItem it = load_item(items, item);
   const int k0 = it.v[0], k1 = it.v[1], q0 = it.v[2], q1 = it.v[3];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int kgrp = kShare ? (wave & 3) : wave;  // this wave's 32 keys
+  const int dpart = kShare ? (wave >> 2) : 0;   // this wave's half of d (kShare)
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const bool wave_active = k0 + wave * 32 < k1;
+  const bool wave_active = k0 + kgrp * 32 < k1;
 
   // stage query block qb: Q and dO rows by 16-byte DMA, LSE and delta (strided
   // by H) by one 4-byte DMA per lane -- even waves LSE, odd waves delta (the
@@ -193,14 +198,14 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   const int nblk = (q1 - q0 + kRB - 1) / kRB;
   if (nblk > 0) issue(q0, 0);
 
-  typename M::v8 kf[NC], vf[NC];
+  typename M::v8 kf[NCS], vf[NCS];
   {
     const int nk = k1 - k0;
     const rsrc_t rk = make_rsrc(k + (int64_t)k0 * H * D, (int64_t)nk * H * D * 2);
     const rsrc_t rv = make_rsrc(v + (int64_t)k0 * H * D, (int64_t)nk * H * D * 2);
-    const int off = ((wave * 32 + lrow) * H + h) * D * 2 + lhalf * 16;
+    const int off = ((kgrp * 32 + lrow) * H + h) * D * 2 + lhalf * 16 + dpart * NDO * 64;
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
+    for (int cc = 0; cc < NCS; ++cc) {
       u32x4 a = buf_load16(rk, off + cc * 32), b = buf_load16(rv, off + cc * 32);
       // waited for here, in the prologue, not inside the loop
       asm volatile("" : "+v"(a), "+v"(b));
@@ -224,7 +229,7 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
 
   // per-lane element offsets: row lrow at d = 8*lhalf (A of S and dP) and the
   // origin of the transposed reads (layout of tr_operand)
-  const int a_off = L::row(lrow) + lhalf * 8;
+  const int a_off = L::row(lrow) + lhalf * 8 + dpart * NDO * 32;
   const int t_off = L::row(4 * (lane >> 5) + ((lane & 15) >> 2)) + ((lane >> 4) & 1) * 16 +
                     4 * (lane & 3);
   // Two query blocks per trip (below), so each block's LDS buffer is a
@@ -234,17 +239,17 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
     wait_vmcnt<0>();
     __syncthreads();  // block j visible; every wave is done with the other buffer
     if (j + 1 < nblk) issue(q0 + (j + 1) * kRB, 1 - B);
+    const unsigned char *base = smem_raw + B * S::kBufBytes;
+    const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
+    const lds_cptr<T> ds_ = qs + S::kQs;
+    const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
+    f32x16 s, dp;
     if (wave_active) {
-      const unsigned char *base = smem_raw + B * S::kBufBytes;
-      const lds_cptr<T> qs = as_lds(reinterpret_cast<const T *>(base));
-      const lds_cptr<T> ds_ = qs + S::kQs;
-      const float *ls = reinterpret_cast<const float *>(base + 2 * S::kQs * 2);
       // S = Q K^T (even reads, Q rows) and dP = dO V^T (odd reads, dO rows);
       // with kDeltaInChain delta - dP = delta + dO (-V)^T, the chain starting
       // from the block's delta (row r of the accumulator is query
-      // 8*(r/4) + 4*lhalf + r%4)
+      // 8*(r/4) + 4*lhalf + r%4); kShare: over this wave's half of d
       auto aop = [&](int i) { return lds_ld16<T>(((i & 1) ? ds_ : qs) + a_off + (i >> 1) * 16); };
-      f32x16 s, dp;
   #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x4 d4 = kDeltaInChain
@@ -261,15 +266,57 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
       for (int i = 0; i < kPre; ++i) ring[i] = aop(i);
       __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
-      for (int i = 0; i < 2 * NC; ++i) {
+      for (int i = 0; i < 2 * NCS; ++i) {
         const typename M::v8 a = as_v8<T>(ring[i % kPre]);
         if (i & 1)
           dp = M::mma(a, vf[i >> 1], dp);
         else
           s = M::mma(a, kf[i >> 1], s);
-        if (i + kPre < 2 * NC) ring[i % kPre] = aop(i + kPre);
+        if (i + kPre < 2 * NCS) ring[i % kPre] = aop(i + kPre);
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (kShare) {
+        // this wave's partial S and dP for the partner wave (wave ^ 4):
+        // [register group][lane] as 16-byte pieces, 1 KiB per instruction
+        // (byte offset formed here, volatile: no address register is held
+        // across the block loop)
+        int eo;
+        asm volatile("v_lshl_add_u32 %0, %1, 4, %2"
+                     : "=v"(eo)
+                     : "v"(lane), "s"(S::kBytes + wave * 8 * 64 * 16));
+        f32x4 *ex = reinterpret_cast<f32x4 *>(smem_raw + eo);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          ex[g * 64] = f32x4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+          ex[(4 + g) * 64] = f32x4{dp[4 * g], dp[4 * g + 1], dp[4 * g + 2], dp[4 * g + 3]};
+        }
+      }
+    }
+    if constexpr (kShare) {
+      // every pair's partial sums written (waves w and w ^ 4 are active
+      // together); the next block's writes come after its first barrier,
+      // when every wave has read these
+      __syncthreads();
+      if (wave_active) {
+        int eo;
+        asm volatile("v_lshl_add_u32 %0, %1, 4, %2"
+                     : "=v"(eo)
+                     : "v"(lane), "s"(S::kBytes + (wave ^ 4) * 8 * 64 * 16));
+        const f32x4 *ex = reinterpret_cast<const f32x4 *>(smem_raw + eo);
+        // S = S_own + S_partner: fp32 addition commutes, so both waves of the
+        // pair hold the same bits of S, dP and hence of P and dS
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 a = ex[g * 64], b = ex[(4 + g) * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[4 * g + e] += a[e];
+            dp[4 * g + e] += b[e];
+          }
+        }
+      }
+    }
+    if (wave_active) {
       // transposed operands: i -> this workgroup's d tile i % NDO, query half
       // mm = (i / NDO) >> 1, dO^T (for dV^T, with P) when (i / NDO) is even,
       // else Q^T (for dK^T, with dS)
@@ -375,8 +422,8 @@ __global__ __launch_bounds__(64 * NW, D >= 256 ? 1 : 2) void varlen_dkv_kernel(
   if (!wave_active) return;
   using SR = StagedRows<T, NDO>;
   unsigned char *stage = smem_raw + wave * SR::kBytes;
-  const int rows = uniform_clamp(k1 - (k0 + wave * 32), 32);
-  const int64_t off = ((int64_t)(k0 + wave * 32) * H + h) * D + dpart * NDO * 32;
+  const int rows = uniform_clamp(k1 - (k0 + kgrp * 32), 32);
+  const int64_t off = ((int64_t)(k0 + kgrp * 32) * H + h) * D + dpart * NDO * 32;
   SR::store(adk, [&](float x) { return static_cast<T>(x * scale); }, stage, dk + off,
             (int64_t)H * D, rows);
   SR::store(adv, [](float x) { return static_cast<T>(x); }, stage, dv + off, (int64_t)H * D,
@@ -917,9 +964,8 @@ template <typename T, int D, int NW>
 void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
   const int smem = dkv_lds_bytes<T, D, NW>();
   allow_dynamic_lds(reinterpret_cast<const void *>(&varlen_dkv_kernel<T, D, NW>), smem);
-  const int64_t dsplit = D >= 256 ? 2 : 1;  // d halves per key tile (see the kernel)
   hipLaunchKernelGGL((varlen_dkv_kernel<T, D, NW>),
-                     dim3((unsigned)(a.n_kv * a.H * dsplit)), dim3(64 * NW), smem, st,
+                     dim3((unsigned)(a.n_kv * a.H)), dim3(64 * NW), smem, st,
                      (const T *)a.q, (const T *)a.k, (const T *)a.v, (const T *)a.dout,
                      a.lse_in, a.delta, (T *)a.dk, (T *)a.dv, a.kv_items, a.H,
                      a.scale * kLog2e, a.scale);
@@ -929,10 +975,14 @@ void launch_dkv_nw(const VarlenArgs &a, hipStream_t st) {
 template <typename T, int D>
 void launch_mfma_varlen_dkv(const VarlenArgs &a, hipStream_t st) {
   if (a.n_kv == 0) return;
-  if constexpr (D == 128) {
-    if (a.k_tile == kVarlenWideTile) return launch_dkv_nw<T, D, 8>(a, st);
+  if constexpr (D == 256) {
+    launch_dkv_nw<T, D, 8>(a, st);  // 128 keys: two waves per 32 keys
+  } else {
+    if constexpr (D == 128) {
+      if (a.k_tile == kVarlenWideTile) return launch_dkv_nw<T, D, 8>(a, st);
+    }
+    launch_dkv_nw<T, D, 4>(a, st);
   }
-  launch_dkv_nw<T, D, 4>(a, st);
 }
 
 template <typename T, int D>

@@ -12,6 +12,7 @@ import torch
 
 from oracle import absorb as oa
 from parity import assert_close
+from varlenabsorbflashattn_amd import _lib
 from varlenabsorbflashattn_amd import (packed_target_attn, prepare_target_attn_indices,
                                        target_attn_inner)
 from varlenabsorbflashattn_amd.workloads import cu_from_lens
@@ -120,6 +121,28 @@ def test_absorb_head_shapes(device, H, D_H, d_kv, dtype):
     print(f"[absorb heads {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
     q_lens, k_lens = [1, 9, 70, 3], [40, 300, 129, 2500]
     got, ref = run_case(q_lens, k_lens, dtype, device, d_q=96, d_kv=d_kv, H=H, D_H=D_H)
+    for n, a, r in zip(NAMES, got, ref):
+        assert_close(n, a, r)
+
+
+# Heads per wave x D_H >= 128 (16-bit, unfolded) writes aX/l and projects it
+# in a row GEMM after the split combine: split key ranges (combined at the
+# padded D_KV width, in W_V's re-laid-out f order), padded D_KV (100 -> 104
+# -> FP 128), H not dividing 64, and the narrower heads that qualify by
+# heads per wave (H = 8, D_H = 64; H = 16, D_H = 32; H = 40, D_H = 16).
+WIDE_SPLIT = [(8, 256, 256), (4, 128, 192), (3, 128, 100), (5, 256, 64), (8, 64, 216),
+              (16, 32, 128), (40, 16, 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("H,D_H,d_kv", WIDE_SPLIT, ids=[f"H{h}_DH{d}_F{f}" for h, d, f in WIDE_SPLIT])
+def test_absorb_wide_dh_split(device, H, D_H, d_kv, dtype):
+    q_lens, k_lens = [3, 40, 0, 9], [5000, 9000, 4, 70]
+    plan = _lib.plan_absorb(cu_from_lens(q_lens).numpy(), cu_from_lens(k_lens).numpy(), H,
+                            d_kv, D_H)
+    assert plan.info.n_comb > 0, "the case must split a key range"
+    print(f"[absorb wide split {dtype}] H={H} D_H={D_H} d_kv={d_kv}", flush=True)
+    got, ref = run_case(q_lens, k_lens, dtype, device, d_q=64, d_kv=d_kv, H=H, D_H=D_H)
     for n, a, r in zip(NAMES, got, ref):
         assert_close(n, a, r)
 

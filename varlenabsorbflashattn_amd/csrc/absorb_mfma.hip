@@ -21,6 +21,15 @@
 // matrix cores -- U^T_h = W_K,h q_proj_h^T per 16-row f tile, accumulated in
 // fp32 over d and rounded once to the input dtype, the reference's u GEMM
 // (ta/interface.py:435) -- so u never reaches HBM.
+//
+// Unprojected epilogue (the DH = 0 instantiation, for wide heads or many
+// heads per wave): each wave would read its heads' W_V (up to 2 x D_KV x D_H
+// at H = 8, 256 KB at D_H = 256) from L2 for only 16 rows, so instead the
+// rounded aX/l rows are written out
+// ([T_q, H, FP] in wvt's f order; split partials unrounded as fp32) and one
+// row GEMM with wvt projects them after the split combine -- the same
+// roundings as the reference's epilogue: aX/l rounded to the input dtype,
+// then one fp32-accumulated product with W_V (ta/kernels.py:274-275).
 #include <algorithm>
 
 #include "absorb_tiles.h"
@@ -339,6 +348,33 @@ __global__ __launch_bounds__(64 * kFwdWaves, 2) void absorb_fwd_kernel(
       part_lse[(int64_t)(pbase + tl) * H + hh] = lse_v;
   }
   if (!wave_active) return;
+  if constexpr (DH == 0) {
+    // unprojected: position 32*kc + 8*lq + t of the row (wvt's f order, as
+    // in bx below) is accumulator element [2kc + t/4][t%4]
+    if (!row_ok) return;
+    if (pbase < 0) {
+      T *dst = O + ((int64_t)(t0 + tl) * H + hh) * FP + lq * 8;
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        v8 b;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(acc[2 * kc + (t >> 2)][t & 3] * inv);
+        *reinterpret_cast<v8 *>(dst + kc * 32) = b;
+      }
+    } else {
+      float *dst = part_o + ((int64_t)(pbase + tl) * H + hh) * FP + lq * 8;
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          f32x4 v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = acc[2 * kc + s][r] * inv;
+          *reinterpret_cast<f32x4 *>(dst + kc * 32 + 4 * s) = v;
+        }
+    }
+    return;
+  }
   // B operand of O^T = W_V^T (aX/l)^T for 32-wide f chunk kc: k slot t of
   // lane group lq is f = 32*kc + 4*lq + t (t < 4, from acc[2kc]) or
   // 32*kc + 16 + 4*lq + t - 4 (t >= 4, from acc[2kc+1]); wvt stores W_V^T in
@@ -386,7 +422,8 @@ void launch_fold(const AbsorbArgs &a, const T *wvt, hipStream_t st) {
   allow_dynamic_lds(reinterpret_cast<const void *>(&absorb_fwd_kernel<T, FP, DH, FOLD>), smem);
   hipLaunchKernelGGL((absorb_fwd_kernel<T, FP, DH, FOLD>), dim3((unsigned)a.n_items),
                      dim3(64 * kFwdWaves), smem, st, (const T *)a.u, (const T *)a.wkt,
-                     (const T *)a.X, wvt, (T *)a.O, a.lse, a.part_o, a.part_lse, a.items, a.H,
+                     (const T *)a.X, wvt, (T *)(DH == 0 ? a.axf : a.O), a.lse, a.part_o,
+                     a.part_lse, a.items, a.H,
                      a.F, a.scale * kLog2e);
 }
 
@@ -469,6 +506,17 @@ bool mfma_absorb_fold_supported(int H, int F, int DH) {
   return padded_f(F) <= 128 || (nhw_t <= 2 && DH <= 64);
 }
 
+// Without the folded projection, shapes whose epilogue would read at least
+// 128 x FP x 2 bytes of W_V per wave (heads per wave x D_H >= 128) write aX/l
+// and project it in a separate row GEMM: per (token, head) row that is 4 FP
+// bytes of HBM traffic (aX written and read back) against heads-per-wave x
+// D_H x FP / 8 bytes of L2 reads, and measured on C4's lengths the row GEMM
+// wins from a ratio of 4 on (H = 8: D_H >= 64; H = 16: D_H >= 32; H <= 4:
+// D_H >= 128).  The combine covers widths up to 256.
+bool mfma_absorb_unprojected(int H, int F, int DH, bool fold) {
+  return absorb_heads_per_wave(H) * DH >= 128 && padded_f(F) <= 256 && !fold;
+}
+
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH) { return (int64_t)H * DH * padded_f(F); }
 int64_t mfma_absorb_wkt_elems(int H, int F, int DH) {
   return (int64_t)H * padded_f(F) * (DH < 32 ? 32 : DH);
@@ -484,6 +532,17 @@ void launch_mfma_absorb_fwd(const AbsorbArgs &a, hipStream_t st) {
                      (const T *)a.wv, wvt, (const T *)a.wk,
                      a.fold ? reinterpret_cast<T *>(a.wkt) : nullptr, a.H, a.F, a.DH, FP, DHP);
   if (a.n_items == 0) return;
+  if (mfma_absorb_unprojected(a.H, a.F, a.DH, a.fold)) {
+    switch (FP) {
+      case 64: launch_fold<T, 64, 0, 0>(a, wvt, st); break;
+      case 128: launch_fold<T, 128, 0, 0>(a, wvt, st); break;
+      case 192: launch_fold<T, 192, 0, 0>(a, wvt, st); break;
+      case 224: launch_fold<T, 224, 0, 0>(a, wvt, st); break;
+      case 256: launch_fold<T, 256, 0, 0>(a, wvt, st); break;
+      default: break;
+    }
+    return;
+  }
   switch (a.DH) {
     case 16: launch_dh<T, 16>(a, wvt, FP, st); break;
     case 32: launch_dh<T, 32>(a, wvt, FP, st); break;

@@ -2,6 +2,7 @@
 // dispatch.  Compiled by hipcc (host code only; kernels live in *.hip).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <initializer_list>
@@ -251,7 +252,7 @@ void varlen_bwd_all(const VarlenArgs &a, hipStream_t st) {
 struct AbsorbWs {
   float *part_o = nullptr, *part_lse = nullptr, *delta = nullptr, *dax = nullptr, *ax = nullptr,
         *dwv_part = nullptr;
-  void *wvt = nullptr, *wkt = nullptr;
+  void *wvt = nullptr, *wkt = nullptr, *axf = nullptr;
   // D_KV padded to a multiple of 8: copies of u, X, W_V and (backward) the
   // padded du, dX, dW_V
   void *pu = nullptr, *pX = nullptr, *pW = nullptr, *pdu = nullptr, *pdX = nullptr,
@@ -300,8 +301,13 @@ AbsorbWs carve_absorb(void *ws, const vafa_plan_info *info, int64_t F0, int64_t 
     }
   }
   if (!bwd) {
-    w.part_o = c.take<float>(info->n_part_rows * H * DH * 4);
+    // the unprojected 16-bit forward keeps split partials and aX/l rows at
+    // the padded D_KV width
+    const bool unproj = !fold && mfma_absorb_unprojected((int)H, (int)F, (int)DH, false);
+    const int64_t fpw = mfma_absorb_wvt_elems(1, (int)F, 1);  // padded D_KV
+    w.part_o = c.take<float>(info->n_part_rows * H * (unproj ? std::max(DH, fpw) : DH) * 4);
     w.part_lse = c.take<float>(info->n_part_rows * H * 4);
+    if (unproj) w.axf = c.take<char>(Tq * H * fpw * 2);
     // W_V re-laid out for the projection: 16-bit (mfma_absorb_wvt_elems x 2
     // bytes) or fp32 (f32_absorb_wvt_elems x 4 bytes); sized for either
     const int64_t wvt16 = mfma_absorb_wvt_elems((int)H, (int)F, (int)DH) * 2;
@@ -326,6 +332,16 @@ void absorb_fwd_all(const AbsorbArgs &a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     if (mfma_absorb_fwd_supported<T>(a.H, a.F, a.DH)) {
       launch_mfma_absorb_fwd<T>(a, st);
+      if (mfma_absorb_unprojected(a.H, a.F, a.DH, a.fold)) {
+        // combine the split partials into the aX/l rows, then O = aX W_V
+        const int FP = (int)mfma_absorb_wvt_elems(1, a.F, 1);
+        launch_lse_combine<T>(a.part_o, a.part_lse, a.axf, a.lse, a.comb_items, a.n_comb, a.H,
+                              FP, a.comb_rows, st);
+        RowGemm p{a.axf, a.wvt, a.O, a.T_q, a.H, a.DH, FP,
+                  (int64_t)a.H * FP, FP, (int64_t)a.DH * FP, FP, (int64_t)a.H * a.DH, a.DH};
+        launch_rowgemm<T>(p, st);
+        return;
+      }
     } else {
       launch_simt_absorb_fwd<T>(a, st);
     }
@@ -727,7 +743,7 @@ int vafa_absorb_fwd(const void *u, const void *X, const void *W_V, void *O, floa
   const hipStream_t st = (hipStream_t)stream;
   AbsorbArgs a{};
   a.u = u; a.X = X; a.wv = W_V; a.O = O; a.lse = lse;
-  a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt;
+  a.part_o = w.part_o; a.part_lse = w.part_lse; a.wvt = w.wvt; a.axf = w.axf;
   int64_t F = D_KV;
   if (absorb_pad(info->H, D_KV, D_H, dtype, false)) {
     F = absorb_fpad(D_KV);

@@ -54,6 +54,9 @@ struct AbsorbArgs {
   float *ax;                  // aX [T_q, H, F] fp32 (backward, for dW_V)
   float *dwv_part;            // [n_tchunks, F, H, D_H] fp32 (backward)
   void *wvt;                  // W_V re-laid out as [H, D_H, F padded to 32] (forward)
+  // forward with mfma_absorb_unprojected: rounded aX/l rows [T_q, H, FP] in
+  // wvt's f order (part_o then holds [rows, H, FP] unprojected partials)
+  void *axf;
   // Folded projection (forward): `u` holds q_proj [T_q, H, D_H] instead of u,
   // and each workgroup forms its rows' u = q_proj_h W_K,h^T from `wk`
   // (W_K [F, H, D_H]) re-laid out into `wkt` ([H, F padded to 32, D_H padded
@@ -139,6 +142,7 @@ template <typename T, int D> void launch_mfma_varlen_fkv(const VarlenArgs &, hip
 template <typename T> bool mfma_absorb_supported(int H, int F, int DH);
 template <typename T> bool mfma_absorb_fwd_supported(int H, int F, int DH);
 int64_t mfma_absorb_wvt_elems(int H, int F, int DH);
+bool mfma_absorb_unprojected(int H, int F, int DH, bool fold);
 bool mfma_absorb_fold_supported(int H, int F, int DH);
 int absorb_heads_per_wave(int H);
 int64_t mfma_absorb_wkt_elems(int H, int F, int DH);

@@ -1,0 +1,121 @@
+"""Packed tensors larger than 4 GiB.
+
+A batch of small segments is packed twice, once at the start of the tensors
+and once after two filler segments that push every tensor past 2^32 bytes:
+one filler with many queries and a single key, one with a single query and
+many keys, so that both the query-side tensors (q, o, dO, dq; absorb u, du)
+and the key-side tensors (k, v, dk, dv; absorb X, dX) hold the far copy past
+4 GiB while the fillers cost little work.  A segment's result depends only on
+its own rows (the plan's tiles, splits and summation orders are fixed per
+segment), so the far copy must reproduce the near copy bit for bit; the near
+copy is held to the oracle with the parity bound.  This pins the kernels'
+row addressing (64-bit row offsets, per-tile buffer descriptors) at the sizes
+an MI355X's 288 GB of HBM allows.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import absorb as oa
+from oracle import varlen as ov
+from parity import assert_close
+from varlenabsorbflashattn_amd import packed_varlen_attn, target_attn_inner
+from varlenabsorbflashattn_amd.workloads import cu_from_lens
+
+pytestmark = pytest.mark.gpu
+
+GIB4 = 1 << 32
+# (queries, keys): a split-K decode segment, a single key, a fused-backward
+# segment (<= 16 queries at D <= 64), tiles with tails, and empty sides
+SMALL = [(37, 300), (1, 5000), (200, 1), (16, 3000), (129, 129), (0, 7), (5, 0)]
+
+
+def _packed(dev, T, shape, dtype, gen, n_small):
+    """Random [T, *shape] with the last n_small rows a copy of the first."""
+    t = torch.empty((T, *shape), device=dev, dtype=dtype)
+    t.normal_(generator=gen)
+    t[T - n_small:] = t[:n_small]
+    return t
+
+
+@pytest.mark.parametrize("H,D,F", [(8, 64, 4_300_000), (16, 128, 1_100_000)],
+                         ids=["h8_d64", "h16_d128"])
+def test_varlen_rows_past_4gib(device, H, D, F):
+    ql, kl = [a for a, _ in SMALL], [b for _, b in SMALL]
+    q_lens, k_lens = ql + [F, 1] + ql, kl + [1, F] + kl
+    Tqs, Tks = sum(ql), sum(kl)
+    Tq, Tk = sum(q_lens), sum(k_lens)
+    row = H * D * 2
+    assert (Tq - Tqs) * row > GIB4 and (Tk - Tks) * row > GIB4
+    print(f"[varlen >4GiB] H={H} D={D} filler={F} T_q={Tq} T_k={Tk} "
+          f"far copy at {(Tq - Tqs) * row / 2**30:.2f} / {(Tk - Tks) * row / 2**30:.2f} GiB",
+          flush=True)
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = _packed(device, Tq, (H, D), torch.bfloat16, gen, Tqs).requires_grad_(True)
+    k = _packed(device, Tk, (H, D), torch.bfloat16, gen, Tks).requires_grad_(True)
+    v = _packed(device, Tk, (H, D), torch.bfloat16, gen, Tks).requires_grad_(True)
+    do = _packed(device, Tq, (H, D), torch.bfloat16, gen, Tqs)
+    cq, ck = cu_from_lens(q_lens, device), cu_from_lens(k_lens, device)
+    scale = 1.0 / math.sqrt(D)
+    o = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck, scale=scale)
+    o.backward(do)
+    torch.cuda.synchronize()
+    print("  ran forward + backward", flush=True)
+    nq, fq = slice(0, Tqs), slice(Tq - Tqs, Tq)
+    nk, fk = slice(0, Tks), slice(Tk - Tks, Tk)
+    for name, t, near, far in (("o", o, nq, fq), ("dq", q.grad, nq, fq),
+                               ("dk", k.grad, nk, fk), ("dv", v.grad, nk, fk)):
+        assert torch.equal(t[near], t[far]), f"{name}: far copy differs from near copy"
+    # the near copy against the oracle
+    host = [t[s].detach().float().cpu().numpy() for t, s in ((q, nq), (k, nk), (v, nk), (do, nq))]
+    cqs, cks = cu_from_lens(ql).numpy(), cu_from_lens(kl).numpy()
+    o_ref, _ = ov.forward(*host[:3], cqs, cks, scale, np.float64)
+    dq_r, dk_r, dv_r = ov.backward(*host, cqs, cks, scale, np.float64)
+    for name, a, r in (("o", o[nq], o_ref), ("dq", q.grad[nq], dq_r), ("dk", k.grad[nk], dk_r),
+                       ("dv", v.grad[nk], dv_r)):
+        assert_close(name, a, r)
+
+
+def test_absorb_rows_past_4gib(device):
+    """Absorb inner op (u given), H=8, D_H=32, D_KV=256: u and du past 4 GiB
+    on the query side, X and dX on the key side.  The fillers' dO is zero, so
+    dW_V is twice the small batch's."""
+    H, D_H, F_KV = 8, 32, 256
+    Fq, Fk = 1_100_000, 8_500_000
+    small = [(a, b) for a, b in SMALL if a == 0 or b > 0]  # absorb: queries need keys
+    ql, kl = [a for a, _ in small], [b for _, b in small]
+    q_lens, k_lens = ql + [Fq, 1] + ql, kl + [1, Fk] + kl
+    Tqs, Tks = sum(ql), sum(kl)
+    Tq, Tk = sum(q_lens), sum(k_lens)
+    assert (Tq - Tqs) * H * F_KV * 2 > GIB4 and (Tk - Tks) * F_KV * 2 > GIB4
+    print(f"[absorb >4GiB] T_q={Tq} T_k={Tk} u far copy at "
+          f"{(Tq - Tqs) * H * F_KV * 2 / 2**30:.2f} GiB, X at {(Tk - Tks) * F_KV * 2 / 2**30:.2f} GiB",
+          flush=True)
+    gen = torch.Generator(device=device).manual_seed(1)
+    u = (_packed(device, Tq, (H, F_KV), torch.bfloat16, gen, Tqs) * 0.1).requires_grad_(True)
+    X = (_packed(device, Tk, (F_KV,), torch.bfloat16, gen, Tks) * 0.1).requires_grad_(True)
+    W_V = (torch.randn(F_KV, H, D_H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+    W_V.requires_grad_(True)
+    dO = torch.zeros(Tq, H, D_H, device=device, dtype=torch.bfloat16)
+    dO[:Tqs] = (torch.randn(Tqs, H, D_H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+    dO[Tq - Tqs:] = dO[:Tqs]
+    cq, ck = cu_from_lens(q_lens, device), cu_from_lens(k_lens, device)
+    scale = 1.0 / math.sqrt(D_H)
+    O = target_attn_inner(u, X, W_V, cq, ck, scale=scale)
+    O.backward(dO)
+    torch.cuda.synchronize()
+    print("  ran forward + backward", flush=True)
+    nq, fq = slice(0, Tqs), slice(Tq - Tqs, Tq)
+    nk, fk = slice(0, Tks), slice(Tk - Tks, Tk)
+    for name, t, near, far in (("O", O, nq, fq), ("du", u.grad, nq, fq), ("dX", X.grad, nk, fk)):
+        assert torch.equal(t[near], t[far]), f"{name}: far copy differs from near copy"
+    host = [t.detach().float().cpu().numpy() for t in (u[nq], X[nk], W_V, dO[nq])]
+    cqs, cks = cu_from_lens(ql).numpy(), cu_from_lens(kl).numpy()
+    O_ref, _ = oa.forward(*host[:3], cqs, cks, scale, np.float64)
+    du_r, dX_r, dWV_r = oa.backward(*host, cqs, cks, scale, np.float64)
+    assert_close("O", O[nq], O_ref)
+    assert_close("du", u.grad[nq], du_r)
+    assert_close("dX", X.grad[nk], dX_r)
+    assert_close("dW_V", W_V.grad, 2.0 * dWV_r)

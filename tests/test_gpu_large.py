@@ -40,23 +40,25 @@ def _packed(dev, T, shape, dtype, gen, n_small):
     return t
 
 
-@pytest.mark.parametrize("H,D,F", [(8, 64, 4_300_000), (16, 128, 1_100_000)],
-                         ids=["h8_d64", "h16_d128"])
-def test_varlen_rows_past_4gib(device, H, D, F):
+@pytest.mark.parametrize("H,D,F,dtype", [(8, 64, 4_300_000, torch.bfloat16),
+                                         (16, 128, 1_100_000, torch.bfloat16),
+                                         (8, 64, 2_200_000, torch.float32)],
+                         ids=["h8_d64", "h16_d128", "h8_d64_fp32"])
+def test_varlen_rows_past_4gib(device, H, D, F, dtype):
     ql, kl = [a for a, _ in SMALL], [b for _, b in SMALL]
     q_lens, k_lens = ql + [F, 1] + ql, kl + [1, F] + kl
     Tqs, Tks = sum(ql), sum(kl)
     Tq, Tk = sum(q_lens), sum(k_lens)
-    row = H * D * 2
+    row = H * D * dtype.itemsize
     assert (Tq - Tqs) * row > GIB4 and (Tk - Tks) * row > GIB4
-    print(f"[varlen >4GiB] H={H} D={D} filler={F} T_q={Tq} T_k={Tk} "
+    print(f"[varlen >4GiB] {dtype} H={H} D={D} filler={F} T_q={Tq} T_k={Tk} "
           f"far copy at {(Tq - Tqs) * row / 2**30:.2f} / {(Tk - Tks) * row / 2**30:.2f} GiB",
           flush=True)
     gen = torch.Generator(device=device).manual_seed(0)
-    q = _packed(device, Tq, (H, D), torch.bfloat16, gen, Tqs).requires_grad_(True)
-    k = _packed(device, Tk, (H, D), torch.bfloat16, gen, Tks).requires_grad_(True)
-    v = _packed(device, Tk, (H, D), torch.bfloat16, gen, Tks).requires_grad_(True)
-    do = _packed(device, Tq, (H, D), torch.bfloat16, gen, Tqs)
+    q = _packed(device, Tq, (H, D), dtype, gen, Tqs).requires_grad_(True)
+    k = _packed(device, Tk, (H, D), dtype, gen, Tks).requires_grad_(True)
+    v = _packed(device, Tk, (H, D), dtype, gen, Tks).requires_grad_(True)
+    do = _packed(device, Tq, (H, D), dtype, gen, Tqs)
     cq, ck = cu_from_lens(q_lens, device), cu_from_lens(k_lens, device)
     scale = 1.0 / math.sqrt(D)
     o = packed_varlen_attn(q, k, v, cu_seqlens_q=cq, cu_seqlens_k=ck, scale=scale)
@@ -78,28 +80,30 @@ def test_varlen_rows_past_4gib(device, H, D, F):
         assert_close(name, a, r)
 
 
-def test_absorb_rows_past_4gib(device):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_absorb_rows_past_4gib(device, dtype):
     """Absorb inner op (u given), H=8, D_H=32, D_KV=256: u and du past 4 GiB
     on the query side, X and dX on the key side.  The fillers' dO is zero, so
     dW_V is twice the small batch's."""
     H, D_H, F_KV = 8, 32, 256
-    Fq, Fk = 1_100_000, 8_500_000
+    e = dtype.itemsize
+    Fq, Fk = 1_100_000 * 2 // e, 8_500_000 * 2 // e
     small = [(a, b) for a, b in SMALL if a == 0 or b > 0]  # absorb: queries need keys
     ql, kl = [a for a, _ in small], [b for _, b in small]
     q_lens, k_lens = ql + [Fq, 1] + ql, kl + [1, Fk] + kl
     Tqs, Tks = sum(ql), sum(kl)
     Tq, Tk = sum(q_lens), sum(k_lens)
-    assert (Tq - Tqs) * H * F_KV * 2 > GIB4 and (Tk - Tks) * F_KV * 2 > GIB4
-    print(f"[absorb >4GiB] T_q={Tq} T_k={Tk} u far copy at "
-          f"{(Tq - Tqs) * H * F_KV * 2 / 2**30:.2f} GiB, X at {(Tk - Tks) * F_KV * 2 / 2**30:.2f} GiB",
+    assert (Tq - Tqs) * H * F_KV * e > GIB4 and (Tk - Tks) * F_KV * e > GIB4
+    print(f"[absorb >4GiB] {dtype} T_q={Tq} T_k={Tk} u far copy at "
+          f"{(Tq - Tqs) * H * F_KV * e / 2**30:.2f} GiB, X at {(Tk - Tks) * F_KV * e / 2**30:.2f} GiB",
           flush=True)
     gen = torch.Generator(device=device).manual_seed(1)
-    u = (_packed(device, Tq, (H, F_KV), torch.bfloat16, gen, Tqs) * 0.1).requires_grad_(True)
-    X = (_packed(device, Tk, (F_KV,), torch.bfloat16, gen, Tks) * 0.1).requires_grad_(True)
-    W_V = (torch.randn(F_KV, H, D_H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+    u = (_packed(device, Tq, (H, F_KV), dtype, gen, Tqs) * 0.1).requires_grad_(True)
+    X = (_packed(device, Tk, (F_KV,), dtype, gen, Tks) * 0.1).requires_grad_(True)
+    W_V = (torch.randn(F_KV, H, D_H, device=device, generator=gen) * 0.1).to(dtype)
     W_V.requires_grad_(True)
-    dO = torch.zeros(Tq, H, D_H, device=device, dtype=torch.bfloat16)
-    dO[:Tqs] = (torch.randn(Tqs, H, D_H, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+    dO = torch.zeros(Tq, H, D_H, device=device, dtype=dtype)
+    dO[:Tqs] = (torch.randn(Tqs, H, D_H, device=device, generator=gen) * 0.1).to(dtype)
     dO[Tq - Tqs:] = dO[:Tqs]
     cq, ck = cu_from_lens(q_lens, device), cu_from_lens(k_lens, device)
     scale = 1.0 / math.sqrt(D_H)

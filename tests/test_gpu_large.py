@@ -123,3 +123,69 @@ def test_absorb_rows_past_4gib(device, dtype):
     assert_close("du", u.grad[nq], du_r)
     assert_close("dX", X.grad[nk], dX_r)
     assert_close("dW_V", W_V.grad, 2.0 * dWV_r)
+
+
+
+def _subset(cu, sel):
+    """Rows of the selected segments (in order) and the subset's cu_seqlens."""
+    rows = np.concatenate([np.arange(cu[i], cu[i + 1]) for i in sel]).astype(np.int64)
+    lens = np.array([cu[i + 1] - cu[i] for i in sel])
+    return rows, cu_from_lens(lens.tolist()).numpy()
+
+
+def test_many_tiny_segments(device):
+    """100,000 segments of 0-4 queries and 0-6 keys (every empty combination
+    included), both operators, forward and backward: plans, grids and combine
+    tables at a segment count far above the benchmark's.  Segments are
+    independent, so 10,000 of them drawn at random are held to the oracle (the
+    oracle's per-segment loop over all of them takes minutes); the absorb
+    dW_V, a sum over every token, is left to the other tests."""
+    rng = np.random.default_rng(5)
+    n = 100_000
+    ql = rng.integers(0, 5, n)
+    kl = rng.integers(0, 7, n)
+    sel = np.sort(rng.choice(n, 10_000, replace=False))
+    H, D = 2, 64
+    print(f"[many segments] n={n} T_q={ql.sum()} T_k={kl.sum()} H={H} D={D}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    q, k, v, do = (torch.randn(int(T), H, D, generator=g).to(torch.bfloat16)
+                   for T in (ql.sum(), kl.sum(), kl.sum(), ql.sum()))
+    cq, ck = cu_from_lens(ql.tolist()), cu_from_lens(kl.tolist())
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = packed_varlen_attn(qd, kd, vd, cu_seqlens_q=cq.to(device), cu_seqlens_k=ck.to(device),
+                           scale=scale)
+    o.backward(do.to(device))
+    torch.cuda.synchronize()
+    rq, cqs = _subset(cq.numpy(), sel)
+    rk, cks = _subset(ck.numpy(), sel)
+    host = [t.float().numpy()[r] for t, r in ((q, rq), (k, rk), (v, rk), (do, rq))]
+    o_ref, _ = ov.forward(*host[:3], cqs, cks, scale, np.float64)
+    dq_r, dk_r, dv_r = ov.backward(*host, cqs, cks, scale, np.float64)
+    tq, tk = torch.from_numpy(rq).to(device), torch.from_numpy(rk).to(device)
+    for name, a, r in (("o", o[tq], o_ref), ("dq", qd.grad[tq], dq_r), ("dk", kd.grad[tk], dk_r),
+                       ("dv", vd.grad[tk], dv_r)):
+        assert_close(name, a, r)
+
+    # absorb: queries need keys (Lq > 0 => Lk > 0, ta/interface.py:109-116)
+    kl_a = np.where(ql > 0, np.maximum(kl, 1), kl)
+    Ha, DH, F = 8, 32, 64
+    print(f"[many samples] n={n} T_q={ql.sum()} T_k={kl_a.sum()} H={Ha} D_KV={F}", flush=True)
+    u = (torch.randn(int(ql.sum()), Ha, F, generator=g) * 0.3).to(torch.bfloat16)
+    X = (torch.randn(int(kl_a.sum()), F, generator=g) * 0.3).to(torch.bfloat16)
+    W_V = (torch.randn(F, Ha, DH, generator=g) * 0.1).to(torch.bfloat16)
+    dO = (torch.randn(int(ql.sum()), Ha, DH, generator=g) * 0.1).to(torch.bfloat16)
+    cka = cu_from_lens(kl_a.tolist())
+    sc = 1.0 / math.sqrt(DH)
+    ud, Xd, Wd = (t.to(device).requires_grad_(True) for t in (u, X, W_V))
+    O = target_attn_inner(ud, Xd, Wd, cq.to(device), cka.to(device), scale=sc)
+    O.backward(dO.to(device))
+    torch.cuda.synchronize()
+    rka, ckas = _subset(cka.numpy(), sel)
+    hs = [u.float().numpy()[rq], X.float().numpy()[rka], W_V.float().numpy(),
+          dO.float().numpy()[rq]]
+    O_ref, _ = oa.forward(*hs[:3], cqs, ckas, sc, np.float64)
+    du_r, dX_r, _ = oa.backward(*hs, cqs, ckas, sc, np.float64)
+    tka = torch.from_numpy(rka).to(device)
+    for name, a, r in (("O", O[tq], O_ref), ("du", ud.grad[tq], du_r), ("dX", Xd.grad[tka], dX_r)):
+        assert_close(name, a, r)
